@@ -1,0 +1,234 @@
+"""HIP decode attention on MI355X through libastckv_hip.so (include/astc_kv_hip.h).
+
+PyTorch-ROCm provides device memory and the stream; every computation runs in
+this package's hand-written gfx950 kernels. There is no CPU or PyTorch
+fallback: if the library or a GPU is missing, the entry points raise.
+
+Reference counterparts: the Metal host's dispatch of attention_split_gqa3 +
+attention_merge (metal/probe_gqa_v10.mm:648-681) and its decode readbacks
+(:258-274).
+"""
+from __future__ import annotations
+
+import ctypes as ct
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from .atlas import Atlas, texel_columns
+
+_LIB = None
+LIB_PATH = Path(__file__).with_name("libastckv_hip.so")
+
+LAYOUTS = {"scalar": 0, "rgba": 1}
+
+
+class AkvAttnParams(ct.Structure):
+    _fields_ = [(name, ct.c_uint32) for name in (
+        "batch", "tokens", "query_heads", "kv_heads", "dim", "page_tokens", "tile_tokens", "splits",
+        "layout", "block_x", "block_y", "atlas_rows", "atlas_cols")]
+
+
+def lib():
+    """Load the HIP extension; raises if it is absent or no GPU is visible."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python astc-kv_amd/build.py`")
+        if not torch.cuda.is_available():
+            raise RuntimeError("astc_kv.gpu needs a ROCm GPU (torch.cuda.is_available() is False)")
+        L = ct.CDLL(str(LIB_PATH))
+        P = ct.POINTER(AkvAttnParams)
+        vp = ct.c_void_p
+        L.akv_hip_decode_attention.argtypes = [P, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        L.akv_hip_attention_split.argtypes = [P, vp, vp, vp, vp, vp, vp, vp, vp]
+        L.akv_hip_attention_merge.argtypes = [P, vp, vp, vp, vp]
+        L.akv_hip_fp16_attention.argtypes = [P, vp, vp, vp, vp, vp, vp, vp]
+        L.akv_hip_decode_values.argtypes = [P, vp, vp, vp]
+        L.akv_hip_decode_blocks.argtypes = [vp, ct.c_size_t, ct.c_uint, ct.c_uint, vp, vp]
+        L.akv_hip_error_string.argtypes = [ct.c_int]
+        L.akv_hip_error_string.restype = ct.c_char_p
+        for f in ("akv_hip_decode_attention", "akv_hip_attention_split", "akv_hip_attention_merge",
+                  "akv_hip_fp16_attention", "akv_hip_decode_values", "akv_hip_decode_blocks"):
+            getattr(L, f).restype = ct.c_int
+        _LIB = L
+    return _LIB
+
+
+def _check(rc: int):
+    if rc:
+        raise RuntimeError(f"libastckv_hip: {lib().akv_hip_error_string(rc).decode()} (code {rc})")
+
+
+def _stream(device) -> ct.c_void_p:
+    return ct.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None):
+    return ct.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _need(t: torch.Tensor, dtype, name: str, shape=None):
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+
+
+MAX_TILE_ELEMS = 16384  # tokens * dim of one in-kernel sub-tile (longer splits loop over sub-tiles)
+
+
+def default_tile(batch: int, kv_heads: int, tokens: int, dim: int, block_y: int = 1,
+                 target_groups: int = 1024) -> int:
+    """Tokens per split: the largest tile (<= 16384/dim, a multiple of block_y)
+    that still gives about `target_groups` workgroups, so all 256 CUs get work."""
+    cap = (MAX_TILE_ELEMS // dim) // block_y * block_y
+    want = -(-tokens * batch * kv_heads // target_groups)
+    tile = max(block_y, -(-want // block_y) * block_y)
+    return min(cap, tile)
+
+
+def tile_for_splits(tokens: int, splits: int, block_y: int, dim: int) -> int:
+    """Tile giving exactly `splits` splits when possible (e.g. T2048 in 8 splits)."""
+    tile = -(-tokens // splits)
+    return -(-tile // block_y) * block_y
+
+
+@dataclass
+class DeviceAtlas:
+    """An Atlas resident in GPU memory."""
+    blocks: torch.Tensor    # uint8 [B, Hkv, rows, cols, 16]
+    scale: torch.Tensor     # float16 [B, Hkv, T]
+    offset: torch.Tensor    # float16 [B, Hkv, T]
+    tokens: int
+    dim: int
+    layout: str
+    block_x: int
+    block_y: int
+    page_tokens: int
+
+    @classmethod
+    def from_host(cls, atlas: Atlas, device="cuda") -> "DeviceAtlas":
+        return cls(torch.from_numpy(np.ascontiguousarray(atlas.blocks)).to(device),
+                   torch.from_numpy(np.ascontiguousarray(atlas.scale)).to(device),
+                   torch.from_numpy(np.ascontiguousarray(atlas.offset)).to(device),
+                   atlas.tokens, atlas.dim, atlas.layout, atlas.block_x, atlas.block_y, atlas.page_tokens)
+
+    @property
+    def batch(self) -> int:
+        return self.blocks.shape[0]
+
+    @property
+    def kv_heads(self) -> int:
+        return self.blocks.shape[1]
+
+    def clone(self) -> "DeviceAtlas":
+        return DeviceAtlas(self.blocks.clone(), self.scale.clone(), self.offset.clone(), self.tokens, self.dim,
+                           self.layout, self.block_x, self.block_y, self.page_tokens)
+
+    def nbytes(self) -> int:
+        return self.blocks.numel() + 2 * self.scale.numel() + 2 * self.offset.numel()
+
+
+def make_params(atlas: DeviceAtlas, query_heads: int, tile: int | None = None) -> AkvAttnParams:
+    b, h = atlas.batch, atlas.kv_heads
+    if tile is None:
+        tile = default_tile(b, h, atlas.tokens, atlas.dim, atlas.block_y)
+    cols = -(-texel_columns(atlas.dim, atlas.layout) // atlas.block_x)
+    if atlas.blocks.shape[3] != cols:
+        raise ValueError("atlas columns do not match dim/layout/footprint")
+    return AkvAttnParams(b, atlas.tokens, query_heads, h, atlas.dim, atlas.page_tokens, tile,
+                         -(-atlas.tokens // tile), LAYOUTS[atlas.layout], atlas.block_x, atlas.block_y,
+                         atlas.blocks.shape[2], cols)
+
+
+def _check_qk(q: torch.Tensor, k: torch.Tensor, b: int, h: int, t: int, d: int):
+    if q.dim() != 3 or q.shape[0] != b or q.shape[2] != d or q.shape[1] % h:
+        raise ValueError(f"q must be [B={b}, Hq, D={d}] with Hq a multiple of {h}")
+    _need(q, torch.float32, "q")
+    _need(k, torch.float16, "k", (b, h, t, d))
+
+
+def attention_split(q, k, atlas: DeviceAtlas, params: AkvAttnParams, partial=None, stats=None):
+    """Split pass only; returns (partial [B,Hq,S,D], stats [B,Hq,S,2])."""
+    b, hq, d = q.shape
+    _check_qk(q, k, atlas.batch, atlas.kv_heads, atlas.tokens, atlas.dim)
+    s = params.splits
+    if partial is None:
+        partial = torch.empty((b, hq, s, d), dtype=torch.float32, device=q.device)
+    if stats is None:
+        stats = torch.empty((b, hq, s, 2), dtype=torch.float32, device=q.device)
+    _check(lib().akv_hip_attention_split(ct.byref(params), _ptr(q), _ptr(k), _ptr(atlas.blocks),
+                                         _ptr(atlas.scale), _ptr(atlas.offset), _ptr(partial), _ptr(stats),
+                                         _stream(q.device)))
+    return partial, stats
+
+
+def attention_merge(params: AkvAttnParams, partial, stats, out=None):
+    b, hq, s, d = partial.shape
+    if out is None:
+        out = torch.empty((b, hq, d), dtype=torch.float32, device=partial.device)
+    _check(lib().akv_hip_attention_merge(ct.byref(params), _ptr(partial), _ptr(stats), _ptr(out),
+                                         _stream(partial.device)))
+    return out
+
+
+def decode_attention(q: torch.Tensor, k: torch.Tensor, atlas: DeviceAtlas, tile: int | None = None,
+                     params: AkvAttnParams | None = None, return_states: bool = False):
+    """One decode step: q [B,Hq,D] f32, k [B,Hkv,T,D] f16, V from the ASTC atlas.
+    Returns out [B,Hq,D] f32 (and (partial, stats) if return_states)."""
+    if params is None:
+        params = make_params(atlas, q.shape[1], tile)
+    partial, stats = attention_split(q, k, atlas, params)
+    out = attention_merge(params, partial, stats)
+    return (out, partial, stats) if return_states else out
+
+
+def fp16_params(batch, kv_heads, query_heads, tokens, dim, tile=None) -> AkvAttnParams:
+    if tile is None:
+        tile = default_tile(batch, kv_heads, tokens, dim, 1)
+    return AkvAttnParams(batch, tokens, query_heads, kv_heads, dim, 0, tile, -(-tokens // tile), 0, 4, 4, 0, 0)
+
+
+def fp16_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tile: int | None = None,
+                   params: AkvAttnParams | None = None, partial=None, stats=None, out=None):
+    """FP16-K/V control: same schedule, V read as restored fp16 [B,Hkv,T,D]."""
+    b, hkv, t, d = k.shape
+    _check_qk(q, k, b, hkv, t, d)
+    _need(v, torch.float16, "v", (b, hkv, t, d))
+    if params is None:
+        params = fp16_params(b, hkv, q.shape[1], t, d, tile)
+    s = params.splits
+    if partial is None:
+        partial = torch.empty((b, q.shape[1], s, d), dtype=torch.float32, device=q.device)
+    if stats is None:
+        stats = torch.empty((b, q.shape[1], s, 2), dtype=torch.float32, device=q.device)
+    if out is None:
+        out = torch.empty((b, q.shape[1], d), dtype=torch.float32, device=q.device)
+    _check(lib().akv_hip_fp16_attention(ct.byref(params), _ptr(q), _ptr(k), _ptr(v), _ptr(partial), _ptr(stats),
+                                        _ptr(out), _stream(q.device)))
+    return out
+
+
+def decode_values(atlas: DeviceAtlas, tile: int | None = None) -> torch.Tensor:
+    """Normalised V as the attention kernel decodes it: float16 [B,Hkv,T,D]."""
+    params = make_params(atlas, atlas.kv_heads, tile)
+    u = torch.empty((atlas.batch, atlas.kv_heads, atlas.tokens, atlas.dim), dtype=torch.float16,
+                    device=atlas.blocks.device)
+    _check(lib().akv_hip_decode_values(ct.byref(params), _ptr(atlas.blocks), _ptr(u), _stream(u.device)))
+    return u
+
+
+def decode_blocks(blocks: torch.Tensor, block_x: int, block_y: int) -> torch.Tensor:
+    """uint8 [n,16] ASTC blocks -> float16 RGBA texels [n, by, bx, 4]."""
+    _need(blocks, torch.uint8, "blocks")
+    n = blocks.numel() // 16
+    out = torch.empty((n, block_y, block_x, 4), dtype=torch.float16, device=blocks.device)
+    _check(lib().akv_hip_decode_blocks(_ptr(blocks), n, block_x, block_y, _ptr(out), _stream(blocks.device)))
+    return out

@@ -1,0 +1,72 @@
+#!/usr/bin/env python3
+"""Build the two native libraries of the astc_kv package in place:
+
+* astc_kv/libakv_astc.so   CPU ASTC codec behind the akv_* bridge (g++)
+* astc_kv/libastckv_hip.so gfx950 decode-attention kernels + C-ABI (hipcc)
+
+Run `python astc-kv_amd/build.py` (both) or with --cpu-only / --hip-only.
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parent
+PKG = HERE / "astc_kv"
+CODEC = HERE / "csrc" / "codec"
+HIP = HERE / "csrc" / "hip"
+INCLUDE = ROOT / "include"
+
+CODEC_SOURCES = ["astc_format.cpp", "astc_decode.cpp", "astc_encode.cpp", "bridge.cpp"]
+HIP_SOURCES = [HIP / "decode_attention.hip", CODEC / "astc_format.cpp"]
+ARCH = os.environ.get("PYTORCH_ROCM_ARCH", "gfx950")
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (ROCm toolchain required to build libastckv_hip.so)")
+
+
+def run(cmd):
+    print("+", " ".join(str(c) for c in cmd), flush=True)
+    subprocess.run([str(c) for c in cmd], check=True)
+
+
+def build_cpu():
+    out = PKG / "libakv_astc.so"
+    run(["g++", "-O3", "-std=c++17", "-Wall", "-Wextra", "-fPIC", "-shared", "-ffp-contract=off",
+         f"-I{INCLUDE}", f"-I{CODEC}", *[CODEC / s for s in CODEC_SOURCES], "-o", out])
+    return out
+
+
+def build_hip():
+    out = PKG / "libastckv_hip.so"
+    tmp = out.with_suffix(".so.tmp")
+    run([hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+         # Packed FP32 instructions are kept out of every kernel.
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         f"-I{INCLUDE}", f"-I{CODEC}", f"-I{HIP}", *HIP_SOURCES, "-o", tmp])
+    tmp.replace(out)
+    return out
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--cpu-only", action="store_true")
+    ap.add_argument("--hip-only", action="store_true")
+    args = ap.parse_args(argv)
+    if not args.hip_only:
+        build_cpu()
+    if not args.cpu_only:
+        build_hip()
+
+
+if __name__ == "__main__":
+    sys.exit(main())

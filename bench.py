@@ -1,0 +1,297 @@
+#!/usr/bin/env python3
+"""Decode-attention benchmark: ASTC-V split-K attention on one MI355X.
+
+Workload (one step = one decode step of the whole batch): T=8192 keys per
+sequence, batch 16, 9 query heads / 3 KV heads, head dim 64, FP16 K, V as an
+ASTC RGBA 6x5 atlas (page 120) with per-token fp16 scale/offset; independent
+seeded K/V per sequence (K ~ N(0,1) with 4 channels x8, V ~ N(0, 0.5), q ~ N(0,1)).
+
+Inputs are resident in HBM. A pool of distinct copies of the KV set (> 512 MB
+in total) is rotated across steps so that the 256 MB Infinity Cache cannot
+hold the working set; every step is timed as split + merge launches replayed
+from a HIP graph, with events on the launch stream.
+
+Prints one JSON line. `value` is the effective bandwidth: algorithmic bytes
+of a step (K + ASTC blocks read + V scale/offset + q + out) / step time.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "astc-kv_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse_args(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--tokens", type=int, default=8192)
+    ap.add_argument("--query-heads", type=int, default=9)
+    ap.add_argument("--kv-heads", type=int, default=3)
+    ap.add_argument("--dim", type=int, default=64)
+    ap.add_argument("--layout", default="rgba")
+    ap.add_argument("--block", default="6x5")
+    ap.add_argument("--page", type=int, default=120)
+    ap.add_argument("--tile", type=int, default=0, help="tokens per split (0 = automatic)")
+    ap.add_argument("--quality", type=float, default=50.0, help="encoder effort for the synthetic V atlas")
+    ap.add_argument("--pool-mb", type=float, default=600.0, help="minimum bytes of distinct KV sets rotated")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--out", default="", help="also write the JSON line to this file")
+    return ap.parse_args(argv)
+
+
+def make_inputs(a, rng_seed=20261201):
+    b, hq, hkv, t, d = a.batch, a.query_heads, a.kv_heads, a.tokens, a.dim
+    q = np.empty((b, hq, d), np.float32)
+    k = np.empty((b, hkv, t, d), np.float16)
+    v = np.empty((b, hkv, t, d), np.float32)
+    for s in range(b):
+        rng = np.random.default_rng(rng_seed + s)
+        q[s] = rng.normal(size=(hq, d))
+        ks = rng.normal(size=(hkv, t, d))
+        ks[..., :4] *= 8.0
+        k[s] = ks
+        v[s] = rng.normal(0.0, 0.5, size=(hkv, t, d))
+    return q, k, v
+
+
+def step_bytes(a, atlas):
+    """Algorithmic bytes of one decode step and of one split launch."""
+    b, hq, hkv, t, d = a.batch, a.query_heads, a.kv_heads, a.tokens, a.dim
+    rows_read = -(-t // atlas.block_y)
+    k_bytes = b * hkv * t * d * 2
+    v_bytes = b * hkv * rows_read * atlas.cols * 16
+    meta = b * hkv * t * 4
+    q_bytes = b * hq * d * 4
+    out_bytes = b * hq * d * 4
+    return {"k": k_bytes, "v_blocks": v_bytes, "v_meta": meta, "q": q_bytes, "out": out_bytes,
+            "step": k_bytes + v_bytes + meta + q_bytes + out_bytes}
+
+
+def time_graph(torch, fn, steps, warmup, use_graph=True):
+    """Average ms per call of fn() over `steps`, replayed from one HIP graph
+    (falls back to eager launches). Returns (ms, mode)."""
+    stream = torch.cuda.current_stream()
+    for _ in range(max(warmup, 1)):
+        fn(0)
+    torch.cuda.synchronize()
+    mode = "eager"
+    graph = None
+    if use_graph:
+        try:
+            s = torch.cuda.Stream()
+            s.wait_stream(stream)
+            with torch.cuda.stream(s):
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=s):
+                    for i in range(steps):
+                        fn(i)
+            stream.wait_stream(s)
+            graph.replay()
+            torch.cuda.synchronize()
+            mode = "hipgraph"
+        except Exception as e:  # noqa: BLE001
+            print(f"# graph capture failed ({e}); timing eager launches", file=sys.stderr)
+            graph = None
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    if graph is not None:
+        graph.replay()
+    else:
+        for i in range(steps):
+            fn(i)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps, mode
+
+
+def cpu_baseline(q, k, v_restored, seconds):
+    """The oracle's NumPy restatement of astc_kv/codec.py:253-267 over the whole
+    batch (V already decoded, as in the reference's CPU path). Returns
+    (median seconds per step with all cores, cores, median with 1 core, reps)."""
+    from threadpoolctl import threadpool_limits
+    from oracle import attention_ref as R
+    kf = k.astype(np.float32)
+    cores = len(os.sched_getaffinity(0))
+    res = {}
+    for n, budget in ((cores, seconds * 0.6), (1, seconds * 0.4)):
+        with threadpool_limits(limits=n):
+            for _ in range(3):
+                R.decode_attention(q, kf, v_restored)
+            times = []
+            start = time.perf_counter()
+            while (time.perf_counter() - start < budget and len(times) < 200) or len(times) < 5:
+                t0 = time.perf_counter()
+                R.decode_attention(q, kf, v_restored)
+                times.append(time.perf_counter() - t0)
+        res[n] = (float(np.median(times)), len(times))
+    return res[cores][0], cores, res[1][0], res[cores][1]
+
+
+def main(argv=None):
+    a = parse_args(argv)
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported (run with --gpus 1)",
+              file=sys.stderr)
+        return 2
+    import torch
+
+    from astc_kv import gpu
+    from astc_kv.atlas import build_atlas
+    from oracle import astc_oracle as O
+    from oracle import attention_ref as R
+
+    bx, by = (int(x) for x in a.block.split("x"))
+    t_setup = time.perf_counter()
+    q, k, v = make_inputs(a)
+    atlas = build_atlas(v, a.layout, (bx, by), a.page, a.quality)
+    setup_s = time.perf_counter() - t_setup
+    dev = gpu.DeviceAtlas.from_host(atlas)
+    qt = torch.from_numpy(q).cuda()
+    kt = torch.from_numpy(k).cuda()
+    tile = a.tile or None
+    params = gpu.make_params(dev, a.query_heads, tile)
+    nbytes = step_bytes(a, atlas)
+    set_bytes = kt.numel() * 2 + dev.nbytes() + qt.numel() * 4
+    pool_n = max(1, int(np.ceil(a.pool_mb * 1e6 / set_bytes)))
+    pool = [(kt, dev)] + [(kt.clone(), dev.clone()) for _ in range(pool_n - 1)]
+    s = params.splits
+    partial = torch.empty((a.batch, a.query_heads, s, a.dim), dtype=torch.float32, device="cuda")
+    stats = torch.empty((a.batch, a.query_heads, s, 2), dtype=torch.float32, device="cuda")
+    out = torch.empty((a.batch, a.query_heads, a.dim), dtype=torch.float32, device="cuda")
+
+    def step(i):
+        kk, dd = pool[i % pool_n]
+        gpu.attention_split(qt, kk, dd, params, partial, stats)
+        gpu.attention_merge(params, partial, stats, out)
+
+    def split_only(i):
+        kk, dd = pool[i % pool_n]
+        gpu.attention_split(qt, kk, dd, params, partial, stats)
+
+    torch.cuda.synchronize()
+    ms_step, mode = time_graph(torch, step, a.steps, a.warmup, not a.no_graph)
+    ms_split, _ = time_graph(torch, split_only, a.steps, a.warmup, not a.no_graph)
+
+    def resident(i):
+        gpu.attention_split(qt, kt, dev, params, partial, stats)
+        gpu.attention_merge(params, partial, stats, out)
+
+    ms_resident, _ = time_graph(torch, resident, a.steps, a.warmup, not a.no_graph)
+
+    # FP16 K/V control on the same workload (V = restored values rounded to fp16).
+    u = gpu.decode_values(dev)
+    v16 = (u.float() * dev.scale.float()[..., None] + dev.offset.float()[..., None]).half()
+    del u
+    fparams = gpu.fp16_params(a.batch, a.kv_heads, a.query_heads, a.tokens, a.dim, params.tile_tokens)
+    fpool = [(kt, v16)] + [(kt.clone(), v16.clone()) for _ in range(max(1, int(np.ceil(
+        a.pool_mb * 1e6 / (kt.numel() * 4)))) - 1)]
+    fpart = torch.empty((a.batch, a.query_heads, fparams.splits, a.dim), dtype=torch.float32, device="cuda")
+    fstat = torch.empty_like(fpart[..., :2])
+
+    def fstep(i):
+        kk, vv = fpool[i % len(fpool)]
+        gpu.fp16_attention(qt, kk, vv, params=fparams, partial=fpart, stats=fstat, out=out)
+
+    ms_fp16, _ = time_graph(torch, fstep, a.steps, a.warmup, not a.no_graph)
+    fp16_bytes = nbytes["k"] * 2 + nbytes["q"] + nbytes["out"]
+
+    # Correctness of the measured configuration on two sequences (oracle decode + NumPy attention).
+    step(0)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    sub = [0, a.batch - 1]
+    from astc_kv.atlas import Atlas
+    small = Atlas(atlas.blocks[sub], atlas.scale[sub], atlas.offset[sub], a.tokens, a.dim, a.layout, bx, by, a.page)
+    tex, _ = O.decode_blocks_fp16(small.blocks.reshape(-1, 16), bx, by)
+    bb, hh, rr, cc = small.blocks.shape[:4]
+    img = tex.reshape(bb, hh, rr, cc, by, bx, 4).transpose(0, 1, 2, 4, 3, 5, 6).reshape(bb, hh, rr * by, cc * bx, 4)
+    img = img[:, :, : a.tokens].astype(np.float32)
+    un = img[..., : a.dim, 0] if a.layout == "scalar" else img[:, :, :, : a.dim // 4].reshape(bb, hh, a.tokens, a.dim)
+    vr = R.restore_token(un, small.scale.astype(np.float32)[..., None], small.offset.astype(np.float32)[..., None])
+    ref = R.decode_attention(q[sub], k[sub].astype(np.float32), vr)
+    max_err = float(np.max(np.abs(got[sub] - ref)))
+    parity = bool(np.allclose(got[sub], ref, rtol=1e-3, atol=2e-3))
+
+    cpu = None
+    if not a.no_cpu:
+        tex_all, _ = O.decode_blocks_fp16(atlas.blocks.reshape(-1, 16), bx, by)
+        bb, hh, rr, cc = atlas.blocks.shape[:4]
+        img = tex_all.reshape(bb, hh, rr, cc, by, bx, 4).transpose(0, 1, 2, 4, 3, 5, 6)
+        img = img.reshape(bb, hh, rr * by, cc * bx, 4)[:, :, : a.tokens].astype(np.float32)
+        un = img[..., : a.dim, 0] if a.layout == "scalar" else img[:, :, :, : a.dim // 4].reshape(
+            bb, hh, a.tokens, a.dim)
+        v_rest = R.restore_token(un, atlas.scale.astype(np.float32)[..., None],
+                                 atlas.offset.astype(np.float32)[..., None])
+        del tex_all, img, un
+        sec, cores, sec1, reps = cpu_baseline(q, k, v_rest, a.cpu_seconds)
+        cpu = {"value": nbytes["step"] / sec / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+               "sample": f"full workload (batch {a.batch}, T{a.tokens}), median of {reps} steps of the oracle's "
+                         f"NumPy attention (astc_kv/codec.py:253-267) on pre-decoded V; {sec*1e6:.0f} us/step "
+                         f"on {cores} cores, {sec1*1e6:.0f} us/step on 1 core",
+               "us_per_step": sec * 1e6, "us_per_step_1core": sec1 * 1e6}
+
+    split_bytes = nbytes["step"] - nbytes["out"] + partial.numel() * 4 + stats.numel() * 4
+    achieved = split_bytes / (ms_split * 1e-3) / 1e9
+    value = nbytes["step"] / (ms_step * 1e-3) / 1e9
+    line = {
+        "metric": "µs per decode-attention step + effective KV GB/s (% HBM peak) at T8192",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 6),
+        "us_per_step": round(ms_step * 1e3, 3),
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 K / ASTC V, fp32 accumulate",
+        "data": "synthetic (seeded Gaussian K/V/q), V encoded by this package's ASTC encoder",
+        "config": {"workload": f"decode attention T{a.tokens} batch {a.batch}, {a.query_heads}q/{a.kv_heads}kv, "
+                               f"D{a.dim}, FP16 K + ASTC {a.layout.upper()} {bx}x{by} V (page {a.page})",
+                   "batch": a.batch, "tokens": a.tokens, "query_heads": a.query_heads, "kv_heads": a.kv_heads,
+                   "dim": a.dim, "layout": a.layout, "block": [bx, by], "tile_tokens": params.tile_tokens,
+                   "splits": params.splits, "pool_sets": pool_n, "timing": mode,
+                   "bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "split_kernel (ASTC V)", "bytes_per_launch": split_bytes,
+                     "us_per_launch": round(ms_split * 1e3, 3)},
+        "cpu_baseline": cpu,
+        "resident_single_set": {"us_per_step": round(ms_resident * 1e3, 3),
+                                "GB/s": round(nbytes["step"] / (ms_resident * 1e-3) / 1e9, 2)},
+        "fp16_control": {"us_per_step": round(ms_fp16 * 1e3, 3), "bytes_per_step": fp16_bytes,
+                         "GB/s": round(fp16_bytes / (ms_fp16 * 1e-3) / 1e9, 2),
+                         "astc_speedup": round(ms_fp16 / ms_step, 4)},
+        "parity": {"sequences_checked": sub, "max_abs_err": max_err, "within_rtol1e-3_atol2e-3": parity},
+        "setup_s": round(setup_s, 2),
+    }
+    text = json.dumps(line)
+    print(text, flush=True)
+    if a.out:
+        Path(a.out).parent.mkdir(parents=True, exist_ok=True)
+        Path(a.out).write_text(text + "\n")
+    return 0 if parity else 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

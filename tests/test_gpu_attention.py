@@ -1,0 +1,170 @@
+"""GPU decode-attention parity against the NumPy oracle.
+
+Tolerance: the north-star bar rtol 1e-3 / atol 2e-3 against the fp32 NumPy
+restatement of astc_kv/codec.py:253-267, on V restored from the oracle's
+decode of the same blocks, plus the reference's own gate, relative L2 <= 1e-4
+against an FP64 reference (metal/probe_gqa_v10.mm:719-725).
+"""
+import numpy as np
+import pytest
+
+from oracle import astc_oracle as O
+from oracle import attention_ref as R
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+RTOL, ATOL, REL_L2 = 1e-3, 2e-3, 1e-4
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    from astc_kv import gpu as G
+    G.lib()
+    return G
+
+
+def oracle_v(atlas):
+    b, h, r, c = atlas.blocks.shape[:4]
+    tex, _ = O.decode_blocks_fp16(atlas.blocks.reshape(-1, 16), atlas.block_x, atlas.block_y)
+    img = tex.reshape(b, h, r, c, atlas.block_y, atlas.block_x, 4).transpose(0, 1, 2, 4, 3, 5, 6)
+    img = img.reshape(b, h, r * atlas.block_y, c * atlas.block_x, 4)[:, :, : atlas.tokens].astype(np.float32)
+    if atlas.layout == "scalar":
+        u = img[..., : atlas.dim, 0]
+    else:
+        u = img[:, :, :, : atlas.dim // 4].reshape(b, h, atlas.tokens, atlas.dim)
+    return R.restore_token(u, atlas.scale.astype(np.float32)[..., None], atlas.offset.astype(np.float32)[..., None])
+
+
+def check(out, q, k, v):
+    ref = R.decode_attention(q, k.astype(np.float32), v)
+    np.testing.assert_allclose(out, ref, rtol=RTOL, atol=ATOL)
+    for b in range(q.shape[0]):
+        ref64 = R.attention_fp64(q[b], k[b].astype(np.float64), v[b])
+        assert R.relative_l2(ref64, out[b]) <= REL_L2
+
+
+def run(G, q, k, atlas, tile=None):
+    from astc_kv.gpu import DeviceAtlas
+    dev = DeviceAtlas.from_host(atlas)
+    out = G.decode_attention(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(), dev, tile)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("name,T", [("t384", 384), ("t391", 391)])
+def test_fixture_attention(gpu, golden, name, T):
+    """Real astcenc payloads, the reference's own q and K (scalar 6x6, 9q/3kv, D64)."""
+    from astc_kv.atlas import atlas_from_manifest
+    atlas, _ = atlas_from_manifest(golden / name)
+    q = np.fromfile(golden / name / "q.f32", "<f4").reshape(1, 9, 64)
+    k = np.fromfile(golden / name / "k.f16", "<f2").reshape(1, 3, T, 64)
+    v_ref = np.fromfile(golden / name / "v_decoded.f32", "<f4").reshape(1, 3, T, 64)
+    assert np.array_equal(oracle_v(atlas).view(np.uint32), v_ref.view(np.uint32))
+    for tile in (6, 30, 36, 96, 252):
+        check(run(gpu, q, k, atlas, tile), q, k, v_ref)
+
+
+def test_t2048_eight_splits(gpu, golden):
+    """T2048 by repeating the T384 block rows, 8 splits (make_traffic_fixture semantics)."""
+    from astc_kv.atlas import atlas_from_manifest, replicate_rows
+    from astc_kv.gpu import tile_for_splits
+    base, _ = atlas_from_manifest(golden / "t384")
+    atlas = replicate_rows(base, 2048)
+    q = np.fromfile(golden / "t384" / "q.f32", "<f4").reshape(1, 9, 64)
+    k0 = np.fromfile(golden / "t384" / "k.f16", "<f2").reshape(1, 3, 384, 64)
+    k = np.ascontiguousarray(k0[:, :, np.arange(2048) % 384])
+    tile = tile_for_splits(2048, 8, 6, 64)
+    assert -(-2048 // tile) == 8
+    check(run(gpu, q, k, atlas, tile), q, k, oracle_v(atlas))
+
+
+def synthetic(rng, b, hq, hkv, t, d, outlier_channels=4, heavy=False):
+    q = rng.normal(size=(b, hq, d)).astype(np.float32)
+    if heavy:
+        k = rng.standard_t(3, size=(b, hkv, t, d))
+    else:
+        k = rng.normal(size=(b, hkv, t, d))
+        k[..., :outlier_channels] *= 8
+    v = rng.normal(0, 0.5, size=(b, hkv, t, d)).astype(np.float32)
+    return q, k.astype(np.float16), v
+
+
+@pytest.mark.parametrize("layout,block,b,hq,hkv,t,d,heavy", [
+    ("rgba", (6, 5), 1, 9, 3, 384, 64, False),     # c1 shape
+    ("rgba", (4, 4), 2, 9, 3, 1000, 64, False),
+    ("scalar", (6, 6), 2, 9, 3, 777, 64, False),
+    ("rgba", (4, 4), 1, 32, 8, 700, 128, True),    # c4 head layout, heavy-tailed K
+    ("rgba", (6, 5), 3, 8, 8, 301, 64, False),     # G = 1
+    ("rgba", (6, 5), 1, 16, 2, 259, 64, False),    # G = 8
+])
+def test_synthetic_attention(gpu, layout, block, b, hq, hkv, t, d, heavy):
+    from astc_kv.atlas import build_atlas
+    rng = np.random.default_rng(t + d)
+    q, k, v = synthetic(rng, b, hq, hkv, t, d, heavy=heavy)
+    atlas = build_atlas(v, layout, block, page_tokens=120, quality=40)
+    vr = oracle_v(atlas)
+    for tile in (None, block[1] * 4):
+        check(run(gpu, q, k, atlas, tile), q, k, vr)
+
+
+def test_split_states_match_oracle(gpu, golden):
+    """partial/stats of every split against the FP64 split-state oracle."""
+    from astc_kv.atlas import atlas_from_manifest
+    from astc_kv.gpu import DeviceAtlas
+    atlas, _ = atlas_from_manifest(golden / "t391")
+    q = np.fromfile(golden / "t391" / "q.f32", "<f4").reshape(1, 9, 64)
+    k = np.fromfile(golden / "t391" / "k.f16", "<f2").reshape(1, 3, 391, 64)
+    tile = 36
+    out, partial, stats = gpu.decode_attention(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(),
+                                               DeviceAtlas.from_host(atlas), tile, return_states=True)
+    partial, stats = partial.cpu().numpy()[0], stats.cpu().numpy()[0]
+    u = oracle_v(atlas)  # restored; use u, s, o separately for the factored form
+    b, h, r, c = atlas.blocks.shape[:4]
+    tex, _ = O.decode_blocks_fp16(atlas.blocks.reshape(-1, 16), 6, 6)
+    img = tex.reshape(b, h, r, c, 6, 6, 4).transpose(0, 1, 2, 4, 3, 5, 6).reshape(b, h, r * 6, c * 6, 4)
+    un = img[0, :, :391, :64, 0].astype(np.float64)
+    m, l, acc = R.split_states(q[0], k[0].astype(np.float64), un, atlas.scale[0].astype(np.float64),
+                               atlas.offset[0].astype(np.float64), tile)
+    np.testing.assert_allclose(stats[..., 0], m, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(stats[..., 1], l, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(partial, acc, rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(R.merge(stats[..., 0].astype(np.float64), stats[..., 1], partial),
+                               out.cpu().numpy()[0], rtol=1e-5, atol=1e-5)
+    assert u.shape == (1, 3, 391, 64)
+
+
+def test_fp16_control(gpu):
+    rng = np.random.default_rng(5)
+    q, k, v = synthetic(rng, 2, 9, 3, 1111, 64)
+    vh = v.astype(np.float16)
+    for tile in (None, 64, 256):
+        out = gpu.fp16_attention(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(),
+                                 torch.from_numpy(vh).cuda(), tile)
+        torch.cuda.synchronize()
+        check(out.cpu().numpy(), q, k, vh.astype(np.float32))
+
+
+def test_full_size_c3_properties(gpu):
+    """T8192 x batch 16 (9q/3kv, D64, RGBA 6x5): finite, each sequence independent
+    (permuting the batch permutes the outputs exactly), oracle parity on a subset."""
+    from astc_kv.atlas import build_atlas
+    from astc_kv.gpu import DeviceAtlas
+    rng = np.random.default_rng(8192)
+    b, t = 16, 8192
+    q, k, v = synthetic(rng, b, 9, 3, t, 64)
+    atlas = build_atlas(v, "rgba", (6, 5), page_tokens=120, quality=10)
+    dev = DeviceAtlas.from_host(atlas)
+    qt, kt = torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda()
+    out = gpu.decode_attention(qt, kt, dev).cpu().numpy()
+    assert np.isfinite(out).all()
+    perm = rng.permutation(b)
+    dev_p = DeviceAtlas(dev.blocks[perm].contiguous(), dev.scale[perm].contiguous(), dev.offset[perm].contiguous(),
+                        t, 64, "rgba", 6, 5, 120)
+    out_p = gpu.decode_attention(qt[perm].contiguous(), kt[perm].contiguous(), dev_p).cpu().numpy()
+    assert np.array_equal(out_p, out[perm])
+    sub = [0, 7, 15]
+    from astc_kv.atlas import Atlas
+    small = Atlas(atlas.blocks[sub], atlas.scale[sub], atlas.offset[sub], t, 64, "rgba", 6, 5, 120)
+    check(out[sub], q[sub], k[sub], oracle_v(small))
