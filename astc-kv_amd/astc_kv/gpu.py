@@ -48,6 +48,8 @@ def lib():
         L.akv_hip_fp16_attention.argtypes = [P, vp, vp, vp, vp, vp, vp, vp]
         L.akv_hip_decode_values.argtypes = [P, vp, vp, vp]
         L.akv_hip_decode_blocks.argtypes = [vp, ct.c_size_t, ct.c_uint, ct.c_uint, vp, vp]
+        L.akv_hip_task_tokens.argtypes = [P, ct.c_int]
+        L.akv_hip_task_tokens.restype = ct.c_int
         L.akv_hip_error_string.argtypes = [ct.c_int]
         L.akv_hip_error_string.restype = ct.c_char_p
         for f in ("akv_hip_decode_attention", "akv_hip_attention_split", "akv_hip_attention_merge",
@@ -81,17 +83,29 @@ def _need(t: torch.Tensor, dtype, name: str, shape=None):
         raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
 
 
-MAX_TILE_ELEMS = 16384  # tokens * dim of one in-kernel sub-tile (longer splits loop over sub-tiles)
+def task_tokens(params: AkvAttnParams, astc: bool = True) -> int:
+    """Tokens per chunk (the unit a workgroup decodes and attends at once)."""
+    rc = lib().akv_hip_task_tokens(ct.byref(params), int(astc))
+    if rc <= 0:
+        _check(rc if rc < 0 else -2)
+    return rc
 
 
-def default_tile(batch: int, kv_heads: int, tokens: int, dim: int, block_y: int = 1,
-                 target_groups: int = 1024) -> int:
-    """Tokens per split: the largest tile (<= 16384/dim, a multiple of block_y)
-    that still gives about `target_groups` workgroups, so all 256 CUs get work."""
-    cap = (MAX_TILE_ELEMS // dim) // block_y * block_y
-    want = -(-tokens * batch * kv_heads // target_groups)
-    tile = max(block_y, -(-want // block_y) * block_y)
-    return min(cap, tile)
+def default_tile(batch: int, kv_heads: int, tokens: int, chunk: int, block: int = 1, cu_count: int = 256) -> int:
+    """Tokens per split (a multiple of `block`, the footprint height).
+
+    Small workloads (fewer chunks than CUs) get splits of about
+    tokens * batch * kv_heads / CUs tokens, at least 16, for parallelism. Otherwise
+    one chunk per split while that gives at most ~4 rounds of 3 resident
+    workgroups per CU; beyond that up to 8 chunks per split, which also cuts
+    the split-state traffic."""
+    seqs = batch * kv_heads
+    total = seqs * -(-tokens // chunk)
+    if total < cu_count:
+        want = max(16, -(-tokens * seqs // cu_count))
+        return min(chunk, -(-want // block) * block)
+    per_split = max(1, min(8, total // (4 * 3 * cu_count)))
+    return per_split * chunk
 
 
 def tile_for_splits(tokens: int, splits: int, block_y: int, dim: int) -> int:
@@ -138,14 +152,19 @@ class DeviceAtlas:
 
 def make_params(atlas: DeviceAtlas, query_heads: int, tile: int | None = None) -> AkvAttnParams:
     b, h = atlas.batch, atlas.kv_heads
-    if tile is None:
-        tile = default_tile(b, h, atlas.tokens, atlas.dim, atlas.block_y)
     cols = -(-texel_columns(atlas.dim, atlas.layout) // atlas.block_x)
     if atlas.blocks.shape[3] != cols:
         raise ValueError("atlas columns do not match dim/layout/footprint")
-    return AkvAttnParams(b, atlas.tokens, query_heads, h, atlas.dim, atlas.page_tokens, tile,
-                         -(-atlas.tokens // tile), LAYOUTS[atlas.layout], atlas.block_x, atlas.block_y,
-                         atlas.blocks.shape[2], cols)
+
+    def build(t):
+        return AkvAttnParams(b, atlas.tokens, query_heads, h, atlas.dim, atlas.page_tokens, t,
+                             -(-atlas.tokens // t), LAYOUTS[atlas.layout], atlas.block_x, atlas.block_y,
+                             atlas.blocks.shape[2], cols)
+
+    if tile is None:
+        whole = -(-atlas.tokens // atlas.block_y) * atlas.block_y   # one split: the chunk is not clipped
+        tile = default_tile(b, h, atlas.tokens, task_tokens(build(whole)), atlas.block_y)
+    return build(tile)
 
 
 def _check_qk(q: torch.Tensor, k: torch.Tensor, b: int, h: int, t: int, d: int):
@@ -191,9 +210,12 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, atlas: DeviceAtlas, tile:
 
 
 def fp16_params(batch, kv_heads, query_heads, tokens, dim, tile=None) -> AkvAttnParams:
+    def build(t):
+        return AkvAttnParams(batch, tokens, query_heads, kv_heads, dim, 0, t, -(-tokens // t), 0, 0, 0, 0, 0)
+
     if tile is None:
-        tile = default_tile(batch, kv_heads, tokens, dim, 1)
-    return AkvAttnParams(batch, tokens, query_heads, kv_heads, dim, 0, tile, -(-tokens // tile), 0, 4, 4, 0, 0)
+        tile = default_tile(batch, kv_heads, tokens, task_tokens(build(tokens), astc=False))
+    return build(tile)
 
 
 def fp16_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tile: int | None = None,

@@ -1,17 +1,22 @@
-// gfx950 software ASTC LDR decode, split in two stages so that a workgroup
-// can decode many blocks in parallel:
-//   1. decode_header: one lane per 16-byte block. Block mode, partitioning,
-//      colour endpoint modes, colour integer-sequence unpack, endpoint
-//      unquantisation and decode -> a BlockDesc in LDS (UNORM16 endpoint pairs
-//      per partition and channel, the bit-reversed weight stream, the
-//      partition pattern, the weight-grid descriptor).
-//   2. decode_texel: one lane per texel. Random-access weight unpack from the
-//      reversed stream (trit/quint block LUTs in LDS), weight infill for
-//      reduced grids, partition lookup, then per channel
-//      C = (e0*(64-w) + e1*w + 32) >> 6 as a single packed-u16 dot product.
-// The result is astcenc's UNORM16 value; unorm16_scaled() maps it to the FP16
-// value astcenc returns (0xFFFF -> 1.0, else c/65536 truncated), which a
-// round-toward-zero FP16 pack (v_cvt_pkrtz_f16_f32) produces exactly.
+// gfx950 software ASTC LDR decode in two stages that each keep a whole
+// workgroup busy.
+//
+//  1. decode_header: one lane per 16-byte block. Block mode, partitioning,
+//     colour endpoint modes, colour integer-sequence (BISE) unpack, endpoint
+//     unquantisation and decode, and the weight BISE unpacked into plain
+//     nb-bit fields (grid order). The result is a 104-byte BlockDesc in LDS.
+//     When the block has an identity weight grid, one plane, and few enough
+//     partitions x weight levels, the header also evaluates every possible
+//     texel value, (partition, weight level) -> FP16 per channel, so that the
+//     texel stage is a table lookup ("table path"). Constant blocks (void
+//     extent, error colour) are one-entry tables.
+//  2. texel_fp16: one lane per texel. Table path: weight field + partition
+//     index -> table entry. Otherwise ("compute path"): weight unquantisation,
+//     bilinear infill for reduced grids, dual-plane selection, and the
+//     interpolation C = (e0*(64-w) + e1*w + 32) >> 6 as one packed-u16 dot
+//     product per channel.
+// Values are astcenc's: UNORM16 C, output FP16 = 1.0 if C == 0xFFFF, else
+// C / 65536 rounded toward zero.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -23,39 +28,51 @@ namespace akv_hip {
 
 using akv::AkvTables;
 
-// Per-texel lookup tables staged in LDS by every workgroup.
+// Per-workgroup lookup tables in LDS.
 struct SmallLuts {
     uint16_t trit[256];
     uint16_t quint[128];
     uint16_t ise[akv::kNumRanges];
-    uint16_t pad[3];
+    uint8_t levels[12];
+    uint8_t pad[6];
     uint8_t wunq[12][32];
 };
 
-// BlockDesc.info bits.
-constexpr uint32_t kInfoDual = 1u << 8;
-constexpr uint32_t kInfoIdentity = 1u << 22;
-constexpr uint32_t kInfoConst = 1u << 23;
+// BlockDesc.info fields (bits 0-3 grid width, 4-7 grid height).
+constexpr uint32_t kInfoDual = 1u << 8;         // bits 9-10: colour component of plane 1
+constexpr int kInfoNbShift = 11;                // bits 11-13: weight field width
+constexpr int kInfoRangeShift = 14;             // bits 14-17: weight range
+constexpr int kInfoLevelsShift = 18;            // bits 18-23: table row length (weight levels)
+constexpr uint32_t kInfoIdentity = 1u << 24;
+constexpr uint32_t kInfoTable = 1u << 25;
 
 template <int NCH>
-struct BlockDesc {
-    uint32_t ep[4][NCH];   // e0 | e1 << 16, UNORM16, per partition and channel
-    uint32_t rev[5];       // block bits reversed (weight stream at bit 0), rev[4] = 0
-    uint32_t part[4];      // 2-bit partition index per texel
-    uint32_t info;         // gw | gh<<4 | dual<<8 | ccs<<9 | wrange<<11 | seqbits<<15 | flags
-    uint32_t pad[2];
+struct alignas(8) BlockDesc {
+    static constexpr int kTabEntries = 32 / NCH;   // 64 bytes of FP16 texel values
+    union {
+        uint32_t ep[4][NCH];   // compute path: e0 | e1 << 16 (UNORM16) per partition and channel
+        uint32_t tab[16];      // table path: entry p * levels + weight field -> NCH fp16
+    };
+    uint32_t qw[5];            // weight fields, nb bits each, grid order (planes interleaved); qw[4] = 0
+    uint32_t part[4];          // 2-bit partition index per texel (texel i: word i / 16, bits 2 * (i % 16))
+    uint32_t info;
 };
-static_assert(sizeof(BlockDesc<4>) % 16 == 0, "desc alignment");
-static_assert(sizeof(BlockDesc<1>) % 16 == 0, "desc alignment");
+static_assert(sizeof(BlockDesc<4>) == 104 && sizeof(BlockDesc<1>) == 104, "BlockDesc layout");
+
+struct Footprint {
+    int bx, by, ntex, ds, dt;   // ds, dt: weight infill steps (1024 + b/2) / (b - 1)
+};
 
 __device__ inline void stage_luts(const AkvTables* __restrict__ tab, SmallLuts& L, int tid, int nthreads) {
+    constexpr uint8_t kLevels[12] = {2, 3, 4, 5, 6, 8, 10, 12, 16, 20, 24, 32};
     for (int i = tid; i < 256; i += nthreads) L.trit[i] = tab->trit[i];
     for (int i = tid; i < 128; i += nthreads) L.quint[i] = tab->quint[i];
     for (int i = tid; i < akv::kNumRanges; i += nthreads) L.ise[i] = tab->ise[i];
+    for (int i = tid; i < 12; i += nthreads) L.levels[i] = kLevels[i];
     for (int i = tid; i < 12 * 32; i += nthreads) (&L.wunq[0][0])[i] = (&tab->weight_unq[0][0])[i];
 }
 
-// Bits [pos, pos+n) of a 128-bit value, n <= 40; bits past 127 read zero.
+// Bits [pos, pos+n) of a 128-bit value, 0 < n <= 40; bits past 127 read zero.
 struct Bits128 {
     uint64_t lo, hi;
     __device__ inline uint64_t get(int pos, int n) const {
@@ -75,7 +92,7 @@ __device__ inline int ise_sequence_bits(int count, int n, bool trit, bool quint)
 }
 
 // Colour value j of this lane's unpacked colour integers (bytes in LDS,
-// column-major [5][nthreads] dwords).
+// column-major [5][stride] dwords).
 __device__ inline int cval(const uint32_t* cv, int stride, int j) {
     return int((cv[(j >> 2) * stride] >> (8 * (j & 3))) & 0xFF);
 }
@@ -168,27 +185,78 @@ __device__ inline bool cem_endpoints(int cem, const uint32_t* cv, int stride, in
     }
 }
 
+// C' for one channel: astcenc's UNORM16 value, except that 0xFFFF becomes
+// 0x10000, so that C' / 65536 rounded toward zero is the FP16 value astcenc
+// returns. With y = dot + 96 = (C + 1) * 64 + r (0 <= r < 64),
+// C' = (y >> 6) + (y >> 22) - 1.
+__device__ inline uint32_t interp_c(uint32_t ep, uint32_t wp) {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const uint32_t y =
+        __builtin_amdgcn_udot2(__builtin_bit_cast(u16x2, ep), __builtin_bit_cast(u16x2, wp), 96u, false);
+    return (y >> 6) + (y >> 22) - 1u;
+}
+
+// Two C' values -> their FP16 values (round toward zero), packed.
+__device__ inline uint32_t pack_fp16_rtz(uint32_t c0, uint32_t c1) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(float(c0) * (1.0f / 65536.0f),
+                                                                   float(c1) * (1.0f / 65536.0f)));
+}
+
+__device__ inline uint32_t weight_pair(int w) { return uint32_t(64 - w) | (uint32_t(w) << 16); }
+
+// The NCH fp16 values of one (partition, weight) as table entry `entry`;
+// entries are 2 * NCH bytes (NCH == 1: two entries share a dword).
+template <int NCH>
+__device__ inline void put_entry(uint32_t* tab, int entry, const uint32_t* ep, uint32_t wp) {
+    if constexpr (NCH == 4) {
+        tab[2 * entry] = pack_fp16_rtz(interp_c(ep[0], wp), interp_c(ep[1], wp));
+        tab[2 * entry + 1] = pack_fp16_rtz(interp_c(ep[2], wp), interp_c(ep[3], wp));
+    } else {
+        reinterpret_cast<uint16_t*>(tab)[entry] = uint16_t(pack_fp16_rtz(interp_c(ep[0], wp), 0));
+    }
+}
+
+// A constant block (void extent or error colour): one table entry.
 template <int NCH>
 __device__ inline void set_constant(BlockDesc<NCH>& d, uint32_t r, uint32_t g, uint32_t b, uint32_t a) {
     const uint32_t c[4] = {r, g, b, a};
+    uint32_t ep[NCH];
 #pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) d.ep[0][ch] = c[ch] | (c[ch] << 16);
+    for (int ch = 0; ch < NCH; ++ch) ep[ch] = c[ch] | (c[ch] << 16);
+    put_entry<NCH>(d.tab, 0, ep, weight_pair(0));
+#pragma unroll
+    for (int i = 0; i < 5; ++i) d.qw[i] = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) d.part[i] = 0;
-    d.info = kInfoConst;
+    d.info = kInfoTable | kInfoIdentity | (1u << kInfoLevelsShift);
 }
 
+// Appends nb-bit fields to the five-word weight stream of a BlockDesc.
+struct FieldWriter {
+    uint32_t* out;
+    uint64_t acc;
+    int bits, words;
+    __device__ inline void put(uint32_t v, int nb) {
+        acc |= uint64_t(v) << bits;
+        bits += nb;
+        if (bits >= 32) {
+            out[words++] = uint32_t(acc);
+            acc >>= 32;
+            bits -= 32;
+        }
+    }
+    __device__ inline void finish() {
+        if (bits > 0) out[words++] = uint32_t(acc);
+        for (; words < 5; ++words) out[words] = 0;
+    }
+};
+
 // Stage 1: one lane decodes one block into `d`. `cv` is this lane's column of
-// a [5][stride] dword scratch array used to hold the unpacked colour values.
+// a [5][stride] dword scratch array for the unpacked colour values.
 template <int NCH>
 __device__ void decode_header(uint4 raw, const AkvTables* __restrict__ tab, const SmallLuts& L, BlockDesc<NCH>& d,
                               uint32_t* cv, int stride) {
     const Bits128 b{uint64_t(raw.x) | (uint64_t(raw.y) << 32), uint64_t(raw.z) | (uint64_t(raw.w) << 32)};
-    d.rev[0] = __builtin_bitreverse32(raw.w);
-    d.rev[1] = __builtin_bitreverse32(raw.z);
-    d.rev[2] = __builtin_bitreverse32(raw.y);
-    d.rev[3] = __builtin_bitreverse32(raw.x);
-    d.rev[4] = 0;
     const uint32_t mode = raw.x & 0x7FF;
     if ((mode & 0x1FF) == 0x1FC) {
         // Void extent: LDR constant colour (UNORM16 RGBA in bits 64..127).
@@ -206,7 +274,8 @@ __device__ void decode_header(uint4 raw, const AkvTables* __restrict__ tab, cons
         set_constant(d, 0xFFFF, 0, 0xFFFF, 0xFFFF);
         return;
     }
-    int below = 128 - int(akv::mode_wbits(md));
+    const int wbits = int(akv::mode_wbits(md));
+    int below = 128 - wbits;
     int color_start = 17, seed = 0;
     uint32_t cems;  // 4 bits per partition
     if (parts == 1) {
@@ -230,8 +299,9 @@ __device__ void decode_header(uint4 raw, const AkvTables* __restrict__ tab, cons
             }
         }
     }
+    const bool dual = akv::mode_dual(md);
     uint32_t ccs = 0;
-    if (akv::mode_dual(md)) {
+    if (dual) {
         below -= 2;
         ccs = uint32_t(b.get(below, 2));
     }
@@ -243,6 +313,10 @@ __device__ void decode_header(uint4 raw, const AkvTables* __restrict__ tab, cons
         set_constant(d, 0xFFFF, 0, 0xFFFF, 0xFFFF);
         return;
     }
+    // Partition pattern, issued before the colour unpack needs its own loads.
+    uint4 pw = uint4{0, 0, 0, 0};
+    if (parts > 1) pw = *reinterpret_cast<const uint4*>(tab->partition[parts - 2][seed]);
+
     // Colour integer sequence -> unquantised bytes, four per scratch dword.
     {
         const int nv = 2 * pairs;
@@ -304,119 +378,145 @@ __device__ void decode_header(uint4 raw, const AkvTables* __restrict__ tab, cons
 #pragma unroll
         for (int i = 0; i < 5; ++i) cv[i * stride] = packed[i];
     }
-    // Endpoints per partition.
-    for (int p = 0, k = 0; p < 4; ++p) {
-        if (p >= parts) break;
+
+    // Weights: the BISE stream runs from bit 127 downwards, so in the
+    // bit-reversed block it starts at bit 0. Unpack it to nb-bit fields.
+    const int wrange = int(akv::mode_range(md));
+    const uint32_t wise = L.ise[wrange];
+    const int n = int(wise & 0xFF);
+    const bool wtrit = (wise >> 8) & 1, wquint = (wise >> 9) & 1;
+    const int nw = int(akv::mode_gw(md) * akv::mode_gh(md)) << (dual ? 1 : 0);
+    const uint32_t rev[5] = {__builtin_bitreverse32(raw.w), __builtin_bitreverse32(raw.z),
+                             __builtin_bitreverse32(raw.y), __builtin_bitreverse32(raw.x), 0u};
+    int nb = n;
+    if (!wtrit && !wquint) {
+        // Plain binary fields are nb-bit fields of the reversed stream already;
+        // fields past the weight count are never read.
+#pragma unroll
+        for (int i = 0; i < 5; ++i) d.qw[i] = rev[i];
+    } else {
+        FieldWriter fw{d.qw, 0, 0, 0};
+        if (wtrit) {
+            nb = n + 2;
+            const int gb = 5 * n + 8;
+            for (int g = 0, pos = 0; 5 * g < nw; ++g, pos += gb) {
+                const int w = pos >> 5;
+                uint32_t G = __builtin_amdgcn_alignbit(rev[w + 1], rev[w], uint32_t(pos & 31));
+                const int len = min(gb, wbits - pos);
+                if (len < 32) G &= (1u << len) - 1;
+                const uint32_t T = __builtin_amdgcn_ubfe(G, n, 2) | __builtin_amdgcn_ubfe(G, 2 * n + 2, 2) << 2 |
+                                   __builtin_amdgcn_ubfe(G, 3 * n + 4, 1) << 4 |
+                                   __builtin_amdgcn_ubfe(G, 4 * n + 5, 2) << 5 |
+                                   __builtin_amdgcn_ubfe(G, 5 * n + 7, 1) << 7;
+                const uint32_t dig = L.trit[T];
+                const int cnt = min(5, nw - 5 * g);
+                for (int j = 0; j < cnt; ++j) {
+                    const int moff = j * n + int((0x75420u >> (4 * j)) & 15);
+                    fw.put((((dig >> (2 * j)) & 3) << n) | __builtin_amdgcn_ubfe(G, moff, n), nb);
+                }
+            }
+        } else {
+            nb = n + 3;
+            const int gb = 3 * n + 7;
+            for (int g = 0, pos = 0; 3 * g < nw; ++g, pos += gb) {
+                const int w = pos >> 5;
+                uint32_t G = __builtin_amdgcn_alignbit(rev[w + 1], rev[w], uint32_t(pos & 31));
+                const int len = min(gb, wbits - pos);
+                if (len < 32) G &= (1u << len) - 1;
+                const uint32_t Q = __builtin_amdgcn_ubfe(G, n, 3) | __builtin_amdgcn_ubfe(G, 2 * n + 3, 2) << 3 |
+                                   __builtin_amdgcn_ubfe(G, 3 * n + 5, 2) << 5;
+                const uint32_t dig = L.quint[Q];
+                const int cnt = min(3, nw - 3 * g);
+                for (int j = 0; j < cnt; ++j) {
+                    const int moff = j * n + int((0x530u >> (4 * j)) & 15);
+                    fw.put((((dig >> (3 * j)) & 7) << n) | __builtin_amdgcn_ubfe(G, moff, n), nb);
+                }
+            }
+        }
+        fw.finish();
+    }
+
+    // Endpoints per partition -> endpoint pairs, or the texel table.
+    const int levels = L.levels[wrange];
+    const bool identity = akv::mode_identity(md);
+    const bool table = identity && !dual && parts * levels <= BlockDesc<NCH>::kTabEntries;
+    for (int p = 0, k = 0; p < parts; ++p) {
         const int cem = int((cems >> (4 * p)) & 15);
         int e0[4], e1[4];
+        uint32_t ep[NCH];
         if (cem_endpoints(cem, cv, stride, k, e0, e1)) {
 #pragma unroll
-            for (int ch = 0; ch < NCH; ++ch) d.ep[p][ch] = uint32_t(e0[ch] * 257) | (uint32_t(e1[ch] * 257) << 16);
+            for (int ch = 0; ch < NCH; ++ch) ep[ch] = uint32_t(e0[ch] * 257) | (uint32_t(e1[ch] * 257) << 16);
         } else {
             const uint32_t err[4] = {0xFFFFFFFFu, 0u, 0xFFFFFFFFu, 0xFFFFFFFFu};
 #pragma unroll
-            for (int ch = 0; ch < NCH; ++ch) d.ep[p][ch] = err[ch];
+            for (int ch = 0; ch < NCH; ++ch) ep[ch] = err[ch];
         }
         k += 2 * ((cem >> 2) + 1);
-    }
-    if (parts > 1) {
-        const uint32_t* pw = tab->partition[parts - 2][seed];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) d.part[i] = pw[i];
-    } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) d.part[i] = 0;
-    }
-    d.info = (md & 0x1FFu) | (ccs << 9) | (akv::mode_range(md) << 11) | (akv::mode_wbits(md) << 15) |
-             (akv::mode_identity(md) ? kInfoIdentity : 0u);
-}
-
-// Unquantised grid weight `idx` (plane-interleaved index) of a block.
-template <int NCH>
-__device__ inline int weight_at(const BlockDesc<NCH>& d, const SmallLuts& L, uint32_t info, int idx) {
-    const int range = int((info >> 11) & 15);
-    const int seq = int((info >> 15) & 127);
-    const uint32_t ise = L.ise[range];
-    const int n = int(ise & 0xFF);
-    int v;
-    if (ise & 0x100) {
-        const int g = idx / 5, j = idx - 5 * g, gb = 5 * n + 8, pos = g * gb;
-        const int w = pos >> 5, sh = pos & 31;
-        uint32_t G = __builtin_amdgcn_alignbit(d.rev[w + 1], d.rev[w], sh);
-        const int len = min(gb, seq - pos);
-        G &= len >= 32 ? 0xFFFFFFFFu : ((1u << len) - 1);
-        uint32_t T = __builtin_amdgcn_ubfe(G, n, 2) | __builtin_amdgcn_ubfe(G, 2 * n + 2, 2) << 2 |
-                     __builtin_amdgcn_ubfe(G, 3 * n + 4, 1) << 4 | __builtin_amdgcn_ubfe(G, 4 * n + 5, 2) << 5 |
-                     __builtin_amdgcn_ubfe(G, 5 * n + 7, 1) << 7;
-        const int moff = j * n + int((0x75420u >> (4 * j)) & 15);
-        v = int(((uint32_t(L.trit[T]) >> (2 * j)) & 3) << n | __builtin_amdgcn_ubfe(G, moff, n));
-    } else if (ise & 0x200) {
-        const int g = idx / 3, j = idx - 3 * g, gb = 3 * n + 7, pos = g * gb;
-        const int w = pos >> 5, sh = pos & 31;
-        uint32_t G = __builtin_amdgcn_alignbit(d.rev[w + 1], d.rev[w], sh);
-        const int len = min(gb, seq - pos);
-        G &= len >= 32 ? 0xFFFFFFFFu : ((1u << len) - 1);
-        uint32_t Q = __builtin_amdgcn_ubfe(G, n, 3) | __builtin_amdgcn_ubfe(G, 2 * n + 3, 2) << 3 |
-                     __builtin_amdgcn_ubfe(G, 3 * n + 5, 2) << 5;
-        const int moff = j * n + int((0x530u >> (4 * j)) & 15);
-        v = int(((uint32_t(L.quint[Q]) >> (3 * j)) & 7) << n | __builtin_amdgcn_ubfe(G, moff, n));
-    } else {
-        const int pos = idx * n, w = pos >> 5, sh = pos & 31;
-        v = int(__builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(d.rev[w + 1], d.rev[w], sh), 0, n));
-    }
-    return L.wunq[range][v];
-}
-
-// Stage 2: UNORM16 value of channels 0..NCH-1 of texel (x, y). `ds`/`dt` are
-// the infill steps (1024 + b/2) / (b - 1) of the footprint.
-template <int NCH>
-__device__ inline void decode_texel(const BlockDesc<NCH>& d, const SmallLuts& L, int x, int y, int bx, int ds,
-                                    int dt, uint32_t* C) {
-    const uint32_t info = d.info;
-    const int i = y * bx + x;
-    uint32_t wp0 = 64, wp1 = 64;  // packed (64 - w) | w << 16 for planes 0 and 1
-    const bool dual = info & kInfoDual;
-    if (!(info & kInfoConst)) {
-        int w0, w1 = 0;
-        if (info & kInfoIdentity) {
-            w0 = weight_at(d, L, info, dual ? 2 * i : i);
-            if (dual) w1 = weight_at(d, L, info, 2 * i + 1);
+        if (table) {
+            for (int q = 0; q < levels; ++q)
+                put_entry<NCH>(d.tab, p * levels + q, ep, weight_pair(L.wunq[wrange][q]));
         } else {
-            const int gw = int(info & 15), gh = int((info >> 4) & 15);
-            const int gs = (ds * x * (gw - 1) + 32) >> 6, gt = (dt * y * (gh - 1) + 32) >> 6;
-            const int fs = gs & 15, ft = gt & 15, base = (gs >> 4) + (gt >> 4) * gw;
-            const int f11 = (fs * ft + 8) >> 4, f01 = fs - f11, f10 = ft - f11, f00 = 16 - fs - ft + f11;
-            const int i01 = f01 ? base + 1 : base, i10 = f10 ? base + gw : base, i11 = f11 ? base + gw + 1 : base;
-            const int planes = dual ? 2 : 1;
-            w0 = (weight_at(d, L, info, base * planes) * f00 + weight_at(d, L, info, i01 * planes) * f01 +
-                  weight_at(d, L, info, i10 * planes) * f10 + weight_at(d, L, info, i11 * planes) * f11 + 8) >> 4;
-            if (dual)
-                w1 = (weight_at(d, L, info, base * 2 + 1) * f00 + weight_at(d, L, info, i01 * 2 + 1) * f01 +
-                      weight_at(d, L, info, i10 * 2 + 1) * f10 + weight_at(d, L, info, i11 * 2 + 1) * f11 + 8) >> 4;
-        }
-        wp0 = uint32_t(64 - w0) | (uint32_t(w0) << 16);
-        wp1 = uint32_t(64 - w1) | (uint32_t(w1) << 16);
-    }
-    const int p = int((d.part[i >> 4] >> (2 * (i & 15))) & 3);
-    const int ccs = dual ? int((info >> 9) & 3) : -1;
-    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) {
-        const uint32_t wp = ch == ccs ? wp1 : wp0;
-        C[ch] = __builtin_amdgcn_udot2(__builtin_bit_cast(u16x2, d.ep[p][ch]), __builtin_bit_cast(u16x2, wp), 32u,
-                                       false) >> 6;
+            for (int ch = 0; ch < NCH; ++ch) d.ep[p][ch] = ep[ch];
+        }
     }
+    d.part[0] = pw.x;
+    d.part[1] = pw.y;
+    d.part[2] = pw.z;
+    d.part[3] = pw.w;
+    d.info = (md & 0xFFu) | (dual ? kInfoDual : 0u) | (ccs << 9) | (uint32_t(nb) << kInfoNbShift) |
+             (uint32_t(wrange) << kInfoRangeShift) | (uint32_t(levels) << kInfoLevelsShift) |
+             (identity ? kInfoIdentity : 0u) | (table ? kInfoTable : 0u);
 }
 
-// UNORM16 -> the FP16 value astcenc outputs, as an exactly representable
-// float: 0xFFFF maps to 1.0, anything else to c/65536 (truncated by the RTZ pack).
-__device__ inline float unorm16_scaled(uint32_t c) {
-    c += (c + 1) >> 16;
-    return float(c) * (1.0f / 65536.0f);
+// Weight field `idx` (grid order, planes interleaved) of a block.
+template <int NCH>
+__device__ inline uint32_t field_at(const BlockDesc<NCH>& d, uint32_t nb, int idx) {
+    const uint32_t pos = uint32_t(idx) * nb, w = pos >> 5;
+    return __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(d.qw[w + 1], d.qw[w], pos & 31), 0, nb);
 }
 
-__device__ inline uint32_t pack_fp16_rtz(uint32_t c0, uint32_t c1) {
-    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(unorm16_scaled(c0), unorm16_scaled(c1)));
+// Unquantised, infilled weight of texel (x, y) on plane `plane` (compute path).
+template <int NCH>
+__device__ inline int texel_weight(const BlockDesc<NCH>& d, const SmallLuts& L, const Footprint& f, uint32_t info,
+                                   int x, int y, int plane) {
+    const uint32_t nb = (info >> kInfoNbShift) & 7;
+    const uint8_t* unq = L.wunq[(info >> kInfoRangeShift) & 15];
+    const int sh = (info & kInfoDual) ? 1 : 0;
+    if (info & kInfoIdentity) return unq[field_at(d, nb, ((y * f.bx + x) << sh) + plane)];
+    const int gw = int(info & 15), gh = int((info >> 4) & 15);
+    const int gs = (f.ds * x * (gw - 1) + 32) >> 6, gt = (f.dt * y * (gh - 1) + 32) >> 6;
+    const int fs = gs & 15, ft = gt & 15, base = (gs >> 4) + (gt >> 4) * gw;
+    const int f11 = (fs * ft + 8) >> 4, f01 = fs - f11, f10 = ft - f11, f00 = 16 - fs - ft + f11;
+    // Taps with a zero factor may lie outside the grid: read the base tap instead.
+    const int i01 = f01 ? base + 1 : base, i10 = f10 ? base + gw : base, i11 = f11 ? base + gw + 1 : base;
+    return (unq[field_at(d, nb, (base << sh) + plane)] * f00 + unq[field_at(d, nb, (i01 << sh) + plane)] * f01 +
+            unq[field_at(d, nb, (i10 << sh) + plane)] * f10 + unq[field_at(d, nb, (i11 << sh) + plane)] * f11 + 8) >>
+           4;
+}
+
+// Stage 2: the FP16 values of texel (x, y) of a block (NCH == 4:
+// {R | G << 16, B | A << 16}; NCH == 1: R in the low half of .x).
+template <int NCH>
+__device__ inline uint2 texel_fp16(const BlockDesc<NCH>& d, const SmallLuts& L, const Footprint& f, int x, int y) {
+    const uint32_t info = d.info;
+    const int i = y * f.bx + x;
+    const int p = int(__builtin_amdgcn_ubfe(d.part[i >> 4], 2 * (i & 15), 2));
+    if (info & kInfoTable) {
+        const uint32_t nb = (info >> kInfoNbShift) & 7;
+        const int entry = p * int((info >> kInfoLevelsShift) & 63) + int(field_at(d, nb, i));
+        if constexpr (NCH == 4) return *reinterpret_cast<const uint2*>(&d.tab[2 * entry]);
+        else return uint2{reinterpret_cast<const uint16_t*>(d.tab)[entry], 0u};
+    }
+    const uint32_t wp0 = weight_pair(texel_weight(d, L, f, info, x, y, 0));
+    const uint32_t wp1 = (info & kInfoDual) ? weight_pair(texel_weight(d, L, f, info, x, y, 1)) : wp0;
+    const int ccs = (info & kInfoDual) ? int((info >> 9) & 3) : 4;
+    uint32_t C[NCH];
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) C[ch] = interp_c(d.ep[p][ch], ch == ccs ? wp1 : wp0);
+    if constexpr (NCH == 4) return uint2{pack_fp16_rtz(C[0], C[1]), pack_fp16_rtz(C[2], C[3])};
+    else return uint2{pack_fp16_rtz(C[0], 0) & 0xFFFFu, 0u};
 }
 
 }  // namespace akv_hip

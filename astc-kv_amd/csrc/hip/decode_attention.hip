@@ -2,22 +2,27 @@
 // FP16-K/V control, the split merge, and the decode readback kernels.
 //
 // Reference semantics: metal/attention_gqa_v10.metal:568-674 (one group per
-// (kv head, split) holding G query states; online softmax; factored token
-// affine acc = sum p*s*u + sum p*o) and :229-253 (exact merge of split states).
+// (kv head, split) holding the G query states of that kv head; online softmax;
+// factored token affine acc = sum p*s*u + sum p*o) and :229-253 (exact merge
+// of split states).
 //
-// Schedule of the split kernel: one 256-lane workgroup per (sequence, kv head,
-// split). It
-//   1. issues the split's K loads (16-byte fp16 loads, 32 KB per workgroup)
-//      into registers first, so HBM latency overlaps the V decode;
-//   2. decodes the split's V blocks into an LDS tile u[tile][dim] (fp16,
-//      exactly the values astcenc returns), one lane per block header, then
-//      one lane per texel;
-//   3. Q.K for all G query heads of the kv head from the staged registers
-//      (each K and V byte is read once per kv head, not once per query head);
-//   4. the split's softmax statistics per head (one wave per head), folding the
-//      per-token V scale into the probabilities;
-//   5. P.V from the LDS tile, reduced across token groups.
-// The merge kernel then combines splits exactly.
+// Split kernel schedule. One 256-lane workgroup per (sequence, kv head,
+// split). A split is processed in chunks of whole block rows (at most 144
+// blocks and 240 tokens for head dim 64). Per chunk:
+//   1. header stage, one lane per block: BlockDesc records in LDS (the
+//      chunk's blocks were loaded one chunk ahead);
+//   2. the chunk's K rows are loaded into registers in the MFMA operand
+//      layout (16-byte loads) while the texel stage runs, and the next
+//      chunk's blocks are requested;
+//   3. texel stage, one lane per pair of tokens: u (the exact FP16 values
+//      astcenc returns) channel-major into the LDS tile vt;
+//   4. each wave takes every fourth 16-token tile: S^T = K.Q^T and O += V^T.P
+//      on the matrix cores (v_mfma_f32_16x16x16_f16, q and p split into fp16
+//      high and low parts so the products keep ~22 bits), the G query heads
+//      padded to the 16 MFMA columns; online softmax per head with the per-token
+//      V scale folded into p and the offset term accumulated separately.
+// At the end the four wave states are combined into the split's state.
+// A second kernel merges the splits.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -32,328 +37,397 @@
 
 namespace akv_hip {
 
-constexpr int kThreads = 256;
-constexpr int kTileElems = 16384;  // tile_tokens * dim per workgroup (32 KB of fp16 K)
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
 
-template <int NCH>
-struct ChunkCap {
-    static constexpr int blocks = NCH == 4 ? 192 : 256;
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+template <int D, int NCH, bool ASTC>
+struct Cfg {
+    static constexpr int kMaxBlocks = ASTC ? 144 : 1;                // blocks per chunk
+    static constexpr int kVtTok = ASTC ? (D == 64 ? 240 : 112) : (D == 64 ? 256 : 128);
+    static constexpr int kVtStride = kVtTok + 4;                     // odd multiple of 8 bytes per row
+    static constexpr int kMaxTiles = kVtTok / 16;                    // 16-token MFMA tiles per chunk
+    static constexpr int kWaveTiles = (kMaxTiles + kWaves - 1) / kWaves;
+    static constexpr int kRowLoads = D / 32;                         // 16-byte row loads per lane per tile
+    static constexpr int kKSteps = D / 16;
+    static constexpr int kMBlocks = D / 16;
+    static_assert((kVtStride / 4) % 2 == 1, "vt rows must be an odd multiple of 8 bytes");
 };
 
-// Per-launch constants derived on the host.
 struct KernelArgs {
     AkvAttnParams p;
-    uint32_t G;        // query heads per kv head
-    int ds, dt;        // weight infill steps
-    uint32_t mag_bx, mag_by, mag_cols;  // ceil(65536 / divisor)
-    float qscale;      // log2(e) / sqrt(dim)
-    uint32_t sub_tokens;  // tokens per in-kernel sub-tile (<= 16384/dim, multiple of block_y)
+    Footprint fp;
+    uint32_t chunk_rows, chunk_tokens;   // block rows / tokens per full chunk
+    uint32_t mag_by, mag_bx;             // ceil(2^24 / divisor)
+    float qscale;                        // log2(e) / sqrt(dim)
 };
 
-__device__ inline uint32_t fdiv(uint32_t a, uint32_t magic) { return (a * magic) >> 16; }
-
+// a / d with magic = ceil(2^24 / d): exact when a * d < 2^24 (the error term
+// a * (magic * d - 2^24) stays below 2^24), which holds for every use below.
+__device__ inline uint32_t fdiv(uint32_t a, uint32_t magic) { return (a * magic) >> 24; }
 __device__ inline float half_to_float(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
 
-__device__ inline float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+// Order this wave's LDS accesses (a wave's LDS operations complete in order).
+__device__ inline void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
 }
 
-template <int D, int NCH, int G>
-struct SplitShared {
-    static constexpr int kMaxTile = kTileElems / D;
-    static constexpr int kCP = D / 2;             // channel pairs
-    static constexpr int kTG = kThreads / kCP;    // PV token groups
-    _Float16 vt[kTileElems];                      // u[tile][D]
-    float sc[G][kMaxTile];                        // scores, then p * scale
-    float qs[G][D];
-    float mlo[G][3];                              // running max, sum, offset term
-    float alpha[G];                               // rescale of the running state
-    SmallLuts luts;
+template <int D, int NCH, bool ASTC>
+struct Shared {
+    using C = Cfg<D, NCH, ASTC>;
     union {
-        struct {
-            BlockDesc<NCH> desc[ChunkCap<NCH>::blocks];
-            uint32_t cv[5][kThreads];
-        } dec;
-        float red[kTG][G][D];
+        _Float16 vt[D][C::kVtStride];   // u (or fp16 V), channel-major
+        float comb[kWaves][D][16];      // final per-wave accumulators
     } u;
+    BlockDesc<NCH> desc[C::kMaxBlocks];
+    uint32_t cv[5][C::kMaxBlocks];      // colour values of the header stage
+    uint32_t so[2][C::kVtTok];          // per-token V scale | offset << 16 (fp16), two chunks
+    SmallLuts luts;
+    float wm[kWaves][16], wl[kWaves][16], wo[kWaves][16];
 };
 
-// Stage 2 of the V decode for one chunk of block rows: every texel of the
-// chunk that maps to a token < nt is written into vt.
-template <int D, int NCH, int G>
-__device__ inline void decode_chunk_texels(SplitShared<D, NCH, G>& sh, const KernelArgs& a, int tid, int chunk_row0,
-                                           int nrows, int nt) {
-    constexpr int TC = NCH == 1 ? D : D / 4;  // texel columns holding channels
-    const int by = int(a.p.block_y), bx = int(a.p.block_x), cols = int(a.p.atlas_cols);
-    const int items = nrows * by * TC;
-    for (int it = tid; it < items; it += kThreads) {
-        const int tl = it / TC, xc = it - tl * TC;
-        const int t_tile = chunk_row0 * by + tl;
-        if (t_tile >= nt) continue;
-        const int brow = int(fdiv(uint32_t(tl), a.mag_by)), y = tl - brow * by;
-        const int bcol = int(fdiv(uint32_t(xc), a.mag_bx)), x = xc - bcol * bx;
-        uint32_t C[NCH];
-        decode_texel<NCH>(sh.u.dec.desc[brow * cols + bcol], sh.luts, x, y, bx, a.ds, a.dt, C);
+// 16-byte rows of one wave's tiles in the MFMA A-operand layout: lane holds
+// token 16 * tile + lane % 16, dims 32 * L + 8 * (lane / 16) .. + 7. Tokens at
+// or past ntok read as zero.
+template <int D, int NCH, bool ASTC>
+__device__ inline void load_rows(uint4* r, const uint16_t* __restrict__ seq, int c0, int ntok, int wave, int lane) {
+    using C = Cfg<D, NCH, ASTC>;
+    const int n16 = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < C::kWaveTiles; ++j)
+#pragma unroll
+        for (int L = 0; L < C::kRowLoads; ++L) {
+            const int tok = 16 * (wave + kWaves * j) + n16;
+            r[j * C::kRowLoads + L] =
+                tok < ntok ? *reinterpret_cast<const uint4*>(seq + size_t(c0 + tok) * D + 32 * L + 8 * g)
+                           : uint4{0, 0, 0, 0};
+        }
+}
+
+// The blocks of the chunk starting at block row `row0` (one per lane).
+template <int D, int NCH>
+__device__ inline uint4 load_block(const KernelArgs& a, const uint4* __restrict__ bseq, int row0, int nrows, int tid) {
+    const int nblk = nrows * int(a.p.atlas_cols);
+    return tid < nblk ? bseq[size_t(row0) * a.p.atlas_cols + tid] : uint4{0, 0, 0, 0};
+}
+
+// Texel stage: one lane per (texel column, token pair) of the chunk; u into vt.
+// Token columns from ntok up to the tile edge are zeroed.
+template <int D, int NCH, bool ASTC>
+__device__ inline void decode_texels(Shared<D, NCH, ASTC>& sh, const KernelArgs& a, int ntok, int tid) {
+    const Footprint& f = a.fp;
+    const int cols = int(a.p.atlas_cols);
+    constexpr int TC = NCH == 1 ? D : D / 4;   // texel columns holding channels
+    const int pairs = 8 * ((ntok + 15) >> 4);
+    const uint32_t mag = (0x1000000u + uint32_t(pairs) - 1) / uint32_t(pairs);
+    for (int it = tid; it < pairs * TC; it += kThreads) {
+        const int x = int(fdiv(uint32_t(it), mag));
+        const int t = 2 * (it - x * pairs);
+        const int bc = int(fdiv(uint32_t(x), a.mag_bx)), xx = x - bc * f.bx;
+        uint2 v[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            v[k] = uint2{0, 0};
+            if (t + k < ntok) {
+                const int r = int(fdiv(uint32_t(t + k), a.mag_by)), y = t + k - r * f.by;
+                v[k] = texel_fp16<NCH>(sh.desc[r * cols + bc], sh.luts, f, xx, y);
+            }
+        }
         if constexpr (NCH == 1) {
-            sh.vt[t_tile * D + xc] = __builtin_bit_cast(_Float16, uint16_t(pack_fp16_rtz(C[0], 0) & 0xFFFF));
+            *reinterpret_cast<uint32_t*>(&sh.u.vt[x][t]) = v[0].x | (v[1].x << 16);
         } else {
-            uint2 h{pack_fp16_rtz(C[0], C[1]), pack_fp16_rtz(C[2], C[3])};
-            *reinterpret_cast<uint2*>(&sh.vt[t_tile * D + 4 * xc]) = h;
+            *reinterpret_cast<uint32_t*>(&sh.u.vt[4 * x + 0][t]) = __builtin_amdgcn_perm(v[1].x, v[0].x, 0x05040100u);
+            *reinterpret_cast<uint32_t*>(&sh.u.vt[4 * x + 1][t]) = __builtin_amdgcn_perm(v[1].x, v[0].x, 0x07060302u);
+            *reinterpret_cast<uint32_t*>(&sh.u.vt[4 * x + 2][t]) = __builtin_amdgcn_perm(v[1].y, v[0].y, 0x05040100u);
+            *reinterpret_cast<uint32_t*>(&sh.u.vt[4 * x + 3][t]) = __builtin_amdgcn_perm(v[1].y, v[0].y, 0x07060302u);
         }
     }
 }
 
-// ASTC: decode V rows of this split into sh.vt. FP16: copy V rows.
-template <int D, int NCH, int G, bool ASTC>
-__device__ inline void stage_v(SplitShared<D, NCH, G>& sh, const KernelArgs& a, const uint4* __restrict__ vblk,
-                               const uint16_t* __restrict__ vh, const AkvTables* __restrict__ tab, int b, int kh,
-                               int t0, int nt, int tid) {
-    const AkvAttnParams& p = a.p;
-    if constexpr (ASTC) {
-        const int by = int(p.block_y), cols = int(p.atlas_cols);
-        const int rows = (nt + by - 1) / by;
-        const int row0 = t0 / by;
-        const int chunk_rows = ChunkCap<NCH>::blocks / cols;
-        const uint4* base = vblk + (size_t(b) * p.kv_heads + kh) * p.atlas_rows * cols;
-        for (int cr = 0; cr < rows; cr += chunk_rows) {
-            const int nrows = min(chunk_rows, rows - cr);
-            const int nblk = nrows * cols;
-            __syncthreads();
-            if (tid < nblk) {
-                const int r = int(fdiv(uint32_t(tid), a.mag_cols));
-                const int c = tid - r * cols;
-                uint4 raw = base[size_t(row0 + cr + r) * cols + c];
-                decode_header<NCH>(raw, tab, sh.luts, sh.u.dec.desc[tid], &sh.u.dec.cv[0][tid], kThreads);
+// FP16 control: transpose this wave's V rows (in registers) into its vt columns.
+template <int D, int NCH, bool ASTC>
+__device__ inline void stage_fp16_rows(Shared<D, NCH, ASTC>& sh, const uint4* v, int wave, int lane) {
+    using C = Cfg<D, NCH, ASTC>;
+    const int n16 = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < C::kWaveTiles; ++j)
+#pragma unroll
+        for (int L = 0; L < C::kRowLoads; ++L) {
+            const uint4 x = v[j * C::kRowLoads + L];
+            const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+            const int tok = 16 * (wave + kWaves * j) + n16, c0 = 32 * L + 8 * g;
+            if (tok < C::kVtTok) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    sh.u.vt[c0 + 2 * i][tok] = __builtin_bit_cast(_Float16, uint16_t(w[i]));
+                    sh.u.vt[c0 + 2 * i + 1][tok] = __builtin_bit_cast(_Float16, uint16_t(w[i] >> 16));
+                }
             }
-            __syncthreads();
-            decode_chunk_texels<D, NCH, G>(sh, a, tid, cr, nrows, nt);
         }
-    } else {
-        const uint4* src = reinterpret_cast<const uint4*>(vh + ((size_t(b) * p.kv_heads + kh) * p.tokens + t0) * D);
-        uint4* dst = reinterpret_cast<uint4*>(sh.vt);
-        for (int i = tid; i < nt * D / 8; i += kThreads) dst[i] = src[i];
-    }
-    __syncthreads();
 }
+
+// --- the split kernel --------------------------------------------------------
 
 template <int D, int NCH, int G, bool ASTC, bool DUMP>
-__global__ __launch_bounds__(kThreads) void split_kernel(KernelArgs a, const float* __restrict__ q,
-                                                         const uint16_t* __restrict__ k,
-                                                         const uint4* __restrict__ vblk,
-                                                         const uint16_t* __restrict__ vh,
-                                                         const uint16_t* __restrict__ vscale,
-                                                         const uint16_t* __restrict__ voffset,
-                                                         const AkvTables* __restrict__ tab,
-                                                         float* __restrict__ partial, float2* __restrict__ stats,
-                                                         uint16_t* __restrict__ dump) {
-    using Sh = SplitShared<D, NCH, G>;
-    __shared__ Sh sh;
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void attn_kernel(
+    KernelArgs a, const float* __restrict__ q, const uint16_t* __restrict__ k, const uint4* __restrict__ vblk,
+    const uint16_t* __restrict__ vh, const uint16_t* __restrict__ vscale, const uint16_t* __restrict__ voffset,
+    const AkvTables* __restrict__ tab, float* __restrict__ partial, float2* __restrict__ stats,
+    uint16_t* __restrict__ dump) {
+    using C = Cfg<D, NCH, ASTC>;
+    __shared__ Shared<D, NCH, ASTC> sh;
     const AkvAttnParams& p = a.p;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int n16 = lane & 15, g = lane >> 4;
     const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
-    const int t_begin = split * int(p.tile_tokens);
-    const int t_end = min(t_begin + int(p.tile_tokens), int(p.tokens));
+    const int T = int(p.tokens);
+    const int split_begin = split * int(p.tile_tokens);
+    const int split_end = min(split_begin + int(p.tile_tokens), T);
+    const int CT = int(a.chunk_tokens);
 
-    constexpr int LPT = D / 8;                 // lanes per token: 8 fp16 channels each
-    constexpr int TPR = kThreads / LPT;        // tokens per round
-    constexpr int ROUNDS = Sh::kMaxTile / TPR;
-    constexpr int CP = Sh::kCP, TG = Sh::kTG;
-    const int tok_lane = tid / LPT, c8 = tid % LPT;
-    const int cp = tid % CP, tg = tid / CP;
-    const int wave = tid >> 6, lane = tid & 63;
+    const size_t seq_kv = size_t(b) * p.kv_heads + kh;
+    const uint16_t* kseq = DUMP ? nullptr : k + seq_kv * p.tokens * D;
+    const uint16_t* vseq = ASTC ? nullptr : vh + seq_kv * p.tokens * D;
+    const uint4* bseq = ASTC ? vblk + seq_kv * p.atlas_rows * p.atlas_cols : nullptr;
+    const uint16_t* sseq = (ASTC && !DUMP) ? vscale + seq_kv * p.tokens : nullptr;
+    const uint16_t* oseq = (ASTC && !DUMP) ? voffset + seq_kv * p.tokens : nullptr;
 
-    if constexpr (!DUMP) {
-        for (int i = tid; i < G * D; i += kThreads)
-            sh.qs[i / D][i % D] = q[(size_t(b) * p.query_heads + size_t(kh) * G) * D + i] * a.qscale;
-        if (tid < G) {
-            sh.mlo[tid][0] = -INFINITY;
-            sh.mlo[tid][1] = 0.0f;
-            sh.mlo[tid][2] = 0.0f;
-        }
+    uint4 raw = uint4{0, 0, 0, 0};
+    if constexpr (ASTC) {
+        const int rows0 = (min(CT, split_end - split_begin) + int(p.block_y) - 1) / int(p.block_y);
+        raw = load_block<D, NCH>(a, bseq, split_begin / int(p.block_y), rows0, tid);
+        stage_luts(tab, sh.luts, tid, kThreads);
     }
-    if constexpr (ASTC) stage_luts(tab, sh.luts, tid, kThreads);
-    float acc[G][2];
-#pragma unroll
-    for (int h = 0; h < G; ++h) acc[h][0] = acc[h][1] = 0.0f;
 
-    // Sub-tiles of at most kMaxTile tokens (a multiple of the block height);
-    // softmax statistics and accumulators are rescaled online across them.
-    for (int s0 = t_begin; s0 < t_end; s0 += int(a.sub_tokens)) {
-        const int nt = min(int(a.sub_tokens), t_end - s0);
-        uint4 kreg[ROUNDS];
-        if constexpr (!DUMP) {
-            const uint16_t* kb = k + ((size_t(b) * p.kv_heads + kh) * p.tokens + s0) * D + c8 * 8;
+    // Q as the B operand of Q.K^T, split into fp16 high and low parts. k-step
+    // ks covers dims 32*(ks/2) + 8*g + 4*(ks%2) + j, matching the K row loads.
+    half4 qhi[C::kKSteps], qlo[C::kKSteps];
 #pragma unroll
-            for (int r = 0; r < ROUNDS; ++r) {
-                const int t = r * TPR + tok_lane;
-                kreg[r] = t < nt ? *reinterpret_cast<const uint4*>(kb + size_t(t) * D) : uint4{0, 0, 0, 0};
-            }
+    for (int ks = 0; ks < C::kKSteps; ++ks)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float v = 0.0f;
+            if (!DUMP && n16 < G)
+                v = q[(size_t(b) * p.query_heads + size_t(kh) * G + n16) * D + 32 * (ks / 2) + 8 * g + 4 * (ks % 2) +
+                      j] *
+                    a.qscale;
+            const _Float16 hi = _Float16(v);
+            qhi[ks][j] = hi;
+            qlo[ks][j] = _Float16(v - float(hi));
         }
-        __syncthreads();  // previous sub-tile's readers of vt/sc are done
-        stage_v<D, NCH, G, ASTC>(sh, a, vblk, vh, tab, b, kh, s0, nt, tid);
 
+    float m_run = -INFINITY, l_run = 0.0f, off_run = 0.0f;
+    floatx4 o[C::kMBlocks];
+#pragma unroll
+    for (int mb = 0; mb < C::kMBlocks; ++mb) o[mb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (ASTC) __syncthreads();   // LUTs staged
+
+    int buf = 0;
+    for (int c0 = split_begin; c0 < split_end; c0 += CT, buf ^= 1) {
+        const int ntok = min(CT, split_end - c0);
+        const int ntiles = (ntok + 15) >> 4;
+        uint4 kreg[C::kWaveTiles * C::kRowLoads];
+        uint4 vreg[ASTC ? 1 : C::kWaveTiles * C::kRowLoads];
+        if constexpr (ASTC) {
+            // Scale/offset of the chunk's tokens (consumed after the next barrier).
+            uint32_t so = 0;
+            if (!DUMP && tid < ntok) so = uint32_t(sseq[c0 + tid]) | (uint32_t(oseq[c0 + tid]) << 16);
+            // 1. Block headers.
+            const int nblk = ((ntok + int(p.block_y) - 1) / int(p.block_y)) * int(p.atlas_cols);
+            if (tid < nblk) decode_header<NCH>(raw, tab, sh.luts, sh.desc[tid], &sh.cv[0][tid], C::kMaxBlocks);
+            // 2. This chunk's K rows, then the next chunk's blocks.
+            if constexpr (!DUMP) load_rows<D, NCH, ASTC>(kreg, kseq, c0, ntok, wave, lane);
+            const int cn = c0 + CT;
+            if (cn < split_end) {
+                const int rows = (min(CT, split_end - cn) + int(p.block_y) - 1) / int(p.block_y);
+                raw = load_block<D, NCH>(a, bseq, cn / int(p.block_y), rows, tid);
+            }
+            if (!DUMP && tid < ntok) sh.so[buf][tid] = so;
+            __syncthreads();
+            // 3. Texels.
+            decode_texels<D, NCH, ASTC>(sh, a, ntok, tid);
+            __syncthreads();
+        } else {
+            load_rows<D, NCH, ASTC>(kreg, kseq, c0, ntok, wave, lane);
+            load_rows<D, NCH, ASTC>(vreg, vseq, c0, ntok, wave, lane);
+            stage_fp16_rows<D, NCH, ASTC>(sh, vreg, wave, lane);
+            wave_sync();
+        }
         if constexpr (DUMP) {
-            uint16_t* dst = dump + ((size_t(b) * p.kv_heads + kh) * p.tokens + s0) * D;
-            const uint16_t* src = reinterpret_cast<const uint16_t*>(sh.vt);
-            for (int i = tid; i < nt * D; i += kThreads) dst[i] = src[i];
+            uint16_t* dst = dump + (seq_kv * p.tokens + c0) * D;
+            for (int i = tid; i < ntok * D; i += kThreads) {
+                const int t = i / D, c = i - t * D;
+                dst[i] = __builtin_bit_cast(uint16_t, sh.u.vt[c][t]);
+            }
+            __syncthreads();
             continue;
         }
 
-        // Q.K from the staged registers.
-        {
-            float qv[G][8];
+        // 4. Scores of this wave's tiles.
+        floatx4 s[C::kWaveTiles];
+        float mt = -INFINITY;
 #pragma unroll
-            for (int h = 0; h < G; ++h)
+        for (int j = 0; j < C::kWaveTiles; ++j) {
+            const int tt = wave + kWaves * j;
+            s[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (tt >= ntiles) continue;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) qv[h][j] = sh.qs[h][c8 * 8 + j];
+            for (int ks = 0; ks < C::kKSteps; ++ks) {
+                const uint4 kk = kreg[j * C::kRowLoads + ks / 2];
+                const half4 ka = __builtin_bit_cast(half4, (ks & 1) ? uint2{kk.z, kk.w} : uint2{kk.x, kk.y});
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(ka, qhi[ks], s[j], 0, 0, 0);
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(ka, qlo[ks], s[j], 0, 0, 0);
+            }
 #pragma unroll
-            for (int r = 0; r < ROUNDS; ++r) {
-                const int t = r * TPR + tok_lane;
-                const uint32_t kw[4] = {kreg[r].x, kreg[r].y, kreg[r].z, kreg[r].w};
-                float kf[8];
+            for (int i = 0; i < 4; ++i) {
+                if (16 * tt + 4 * g + i >= ntok) s[j][i] = -INFINITY;
+                mt = fmaxf(mt, s[j][i]);
+            }
+        }
+        if (wave < ntiles) {
+            mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+            mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+            const float m_new = fmaxf(m_run, mt);
+            const float alpha = exp2f(m_run - m_new);
+            m_run = m_new;
+            l_run *= alpha;
+            off_run *= alpha;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    kf[2 * j] = half_to_float(uint16_t(kw[j] & 0xFFFF));
-                    kf[2 * j + 1] = half_to_float(uint16_t(kw[j] >> 16));
+            for (int mb = 0; mb < C::kMBlocks; ++mb) o[mb] *= alpha;
+#pragma unroll
+            for (int j = 0; j < C::kWaveTiles; ++j) {
+                const int tt = wave + kWaves * j;
+                if (tt >= ntiles) break;
+                uint4 so4 = uint4{0x3C00u, 0, 0x3C00u, 0};   // FP16 control: scale 1, offset 0
+                if constexpr (ASTC) so4 = *reinterpret_cast<const uint4*>(&sh.so[buf][16 * tt + 4 * g]);
+                const uint32_t sov[4] = {so4.x, so4.y, so4.z, so4.w};
+                half4 phi, plo;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float pr = exp2f(s[j][i] - m_new);
+                    l_run += pr;
+                    float pv = pr;
+                    if constexpr (ASTC) {
+                        pv = pr * half_to_float(uint16_t(sov[i]));
+                        off_run = fmaf(pr, half_to_float(uint16_t(sov[i] >> 16)), off_run);
+                    }
+                    const _Float16 h = _Float16(pv);
+                    phi[i] = h;
+                    plo[i] = _Float16(pv - float(h));
                 }
 #pragma unroll
-                for (int h = 0; h < G; ++h) {
-                    float s = 0.0f;
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) s = fmaf(qv[h][j], kf[j], s);
-#pragma unroll
-                    for (int o = 1; o < LPT; o <<= 1) s += __shfl_xor(s, o, 64);
-                    if (c8 == 0 && t < nt) sh.sc[h][t] = s;
+                for (int mb = 0; mb < C::kMBlocks; ++mb) {
+                    const half4 va = *reinterpret_cast<const half4*>(&sh.u.vt[16 * mb + n16][16 * tt + 4 * g]);
+                    o[mb] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, phi, o[mb], 0, 0, 0);
+                    o[mb] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, plo, o[mb], 0, 0, 0);
                 }
             }
         }
-        __syncthreads();
-
-        // Online softmax update per head; fold the per-token V scale into p.
-        const size_t meta = (size_t(b) * p.kv_heads + kh) * p.tokens + s0;
-        for (int h = wave; h < G; h += kThreads / 64) {
-            float m = -INFINITY;
-            for (int t = lane; t < nt; t += 64) m = fmaxf(m, sh.sc[h][t]);
-            const float m_old = sh.mlo[h][0];
-            const float m_new = fmaxf(m_old, wave_max(m));
-            float l = 0.0f, off = 0.0f;
-            for (int t = lane; t < nt; t += 64) {
-                const float pr = exp2f(sh.sc[h][t] - m_new);
-                l += pr;
-                if constexpr (ASTC) {
-                    sh.sc[h][t] = pr * half_to_float(vscale[meta + t]);
-                    off = fmaf(pr, half_to_float(voffset[meta + t]), off);
-                } else {
-                    sh.sc[h][t] = pr;
-                }
-            }
-            l = wave_sum(l);
-            off = wave_sum(off);
-            if (lane == 0) {
-                const float alpha = exp2f(m_old - m_new);
-                sh.alpha[h] = alpha;
-                sh.mlo[h][0] = m_new;
-                sh.mlo[h][1] = fmaf(sh.mlo[h][1], alpha, l);
-                sh.mlo[h][2] = fmaf(sh.mlo[h][2], alpha, off);
-            }
-        }
-        __syncthreads();
-
-        // P.V over the LDS tile: lane = channel pair, token groups reduced at the end.
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            const float alpha = sh.alpha[h];
-            acc[h][0] *= alpha;
-            acc[h][1] *= alpha;
-        }
-        for (int t = tg; t < nt; t += TG) {
-            const uint32_t u2 = *reinterpret_cast<const uint32_t*>(&sh.vt[t * D + 2 * cp]);
-            const float u0 = half_to_float(uint16_t(u2 & 0xFFFF)), u1 = half_to_float(uint16_t(u2 >> 16));
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                const float w = sh.sc[h][t];
-                acc[h][0] = fmaf(w, u0, acc[h][0]);
-                acc[h][1] = fmaf(w, u1, acc[h][1]);
-            }
-        }
+        if constexpr (!ASTC) wave_sync();   // this wave's vt columns are rewritten next chunk
     }
     if constexpr (DUMP) return;
 
-    // The decode scratch is dead now; reuse it for the token-group reduction.
-    __syncthreads();
+    // Wave state: sums over the four lane groups; accumulators to LDS.
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+    off_run += __shfl_xor(off_run, 16, 64);
+    off_run += __shfl_xor(off_run, 32, 64);
+    __syncthreads();   // every wave is done with vt
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-        sh.u.red[tg][h][2 * cp] = acc[h][0];
-        sh.u.red[tg][h][2 * cp + 1] = acc[h][1];
+    for (int mb = 0; mb < C::kMBlocks; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sh.u.comb[wave][16 * mb + 4 * g + i][n16] = o[mb][i];
+    if (g == 0) {
+        sh.wm[wave][n16] = m_run;
+        sh.wl[wave][n16] = l_run;
+        sh.wo[wave][n16] = off_run;
     }
     __syncthreads();
+
+    // Combine the four waves -> this split's state.
     const int S = int(p.splits);
     for (int i = tid; i < G * D; i += kThreads) {
-        const int h = i / D, dd = i % D;
-        float s = 0.0f;
+        const int h = i / D, c = i - h * D;
+        float M = -INFINITY;
 #pragma unroll
-        for (int g = 0; g < TG; ++g) s += sh.u.red[g][h][dd];
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sh.wm[w][h]);
+        float acc = 0.0f, l = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float e = sh.wm[w][h] == -INFINITY ? 0.0f : exp2f(sh.wm[w][h] - M);
+            acc = fmaf(e, sh.u.comb[w][c][h] + sh.wo[w][h], acc);
+            l = fmaf(e, sh.wl[w][h], l);
+        }
         const size_t qh = size_t(b) * p.query_heads + size_t(kh) * G + h;
-        partial[(qh * S + split) * D + dd] = s + sh.mlo[h][2];
-    }
-    if (tid < G) {
-        const size_t qh = size_t(b) * p.query_heads + size_t(kh) * G + tid;
-        // Natural-log max for drop-in statistics: m2 * ln(2).
-        stats[qh * S + split] = float2{sh.mlo[tid][0] * 0.69314718055994531f, sh.mlo[tid][1]};
+        partial[(qh * S + split) * D + c] = acc;
+        if (c == 0) stats[qh * S + split] = float2{M * 0.69314718055994531f, l};
     }
 }
 
-__global__ void merge_kernel(uint32_t splits, uint32_t dim, const float* __restrict__ partial,
-                             const float2* __restrict__ stats, float* __restrict__ out) {
+// Merge: one workgroup per (sequence, query head); wave w takes splits
+// w, w + 4, ...; lane = channel (and channel + 64 for dim 128).
+__global__ __launch_bounds__(kThreads) void merge_kernel(uint32_t splits, uint32_t dim,
+                                                         const float* __restrict__ partial,
+                                                         const float2* __restrict__ stats, float* __restrict__ out) {
+    __shared__ float red_m[kWaves], red_l[kWaves];
+    __shared__ float red_acc[kWaves][128];
     const size_t qh = blockIdx.x;
-    const int d = threadIdx.x;
-    if (d >= int(dim)) return;
-    const float2* st = stats + qh * splits;
-    float m = -INFINITY;
-    for (uint32_t s = 0; s < splits; ++s) m = fmaxf(m, st[s].x);
-    float acc = 0.0f, l = 0.0f;
-    for (uint32_t s = 0; s < splits; ++s) {
-        const float w = st[s].x == -INFINITY ? 0.0f : expf(st[s].x - m);
-        l = fmaf(st[s].y, w, l);
-        acc = fmaf(partial[(qh * splits + s) * dim + d], w, acc);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int S = int(splits), D = int(dim);
+    const float2* st = stats + qh * S;
+    float M = -INFINITY;
+    for (int s = tid; s < S; s += kThreads) M = fmaxf(M, st[s].x);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    if (lane == 0) red_m[wave] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+    const float* base = partial + qh * S * D;
+    float acc0 = 0.0f, acc1 = 0.0f, l = 0.0f;
+#pragma unroll 4
+    for (int s = wave; s < S; s += kWaves) {
+        const float2 ms = st[s];
+        const float e = ms.x == -INFINITY ? 0.0f : expf(ms.x - M);
+        l = fmaf(ms.y, e, l);
+        acc0 = fmaf(base[size_t(s) * D + lane], e, acc0);
+        if (D == 128) acc1 = fmaf(base[size_t(s) * D + 64 + lane], e, acc1);
     }
-    out[qh * dim + d] = acc / l;
+    if (lane == 0) red_l[wave] = l;
+    red_acc[wave][lane] = acc0;
+    if (D == 128) red_acc[wave][64 + lane] = acc1;
+    __syncthreads();
+    if (tid < D) {
+        const float L = red_l[0] + red_l[1] + red_l[2] + red_l[3];
+        const float A = red_acc[0][tid] + red_acc[1][tid] + red_acc[2][tid] + red_acc[3][tid];
+        out[qh * D + tid] = A / L;
+    }
 }
 
-// Standalone block decode: 192 blocks per workgroup -> FP16 RGBA texels.
+// Standalone block decode: 256 blocks per workgroup -> FP16 RGBA texels.
 struct BlocksShared {
     SmallLuts luts;
-    BlockDesc<4> desc[ChunkCap<4>::blocks];
+    BlockDesc<4> desc[kThreads];
     uint32_t cv[5][kThreads];
 };
 
 __global__ __launch_bounds__(kThreads) void decode_blocks_kernel(const uint4* __restrict__ blocks, size_t n,
-                                                                 int bx, int by, int ds, int dt,
-                                                                 const AkvTables* __restrict__ tab,
+                                                                 Footprint f, const AkvTables* __restrict__ tab,
                                                                  uint2* __restrict__ out) {
     __shared__ BlocksShared sh;
-    constexpr int NB = ChunkCap<4>::blocks;
     const int tid = threadIdx.x;
-    const size_t first = size_t(blockIdx.x) * NB;
-    const int nblk = int(min(size_t(NB), n - first));
     stage_luts(tab, sh.luts, tid, kThreads);
     __syncthreads();
+    const size_t first = size_t(blockIdx.x) * kThreads;
+    const int nblk = int(min(size_t(kThreads), n - first));
     if (tid < nblk) decode_header<4>(blocks[first + tid], tab, sh.luts, sh.desc[tid], &sh.cv[0][tid], kThreads);
     __syncthreads();
-    const int per = bx * by;
-    for (int it = tid; it < nblk * per; it += kThreads) {
-        const int blk = it / per, i = it - blk * per;
-        const int y = i / bx, x = i - y * bx;
-        uint32_t C[4];
-        decode_texel<4>(sh.desc[blk], sh.luts, x, y, bx, ds, dt, C);
-        out[(first + blk) * per + i] = uint2{pack_fp16_rtz(C[0], C[1]), pack_fp16_rtz(C[2], C[3])};
+    for (int it = tid; it < nblk * f.ntex; it += kThreads) {
+        const int blk = it / f.ntex, i = it - blk * f.ntex;
+        const int y = i / f.bx, x = i - y * f.bx;
+        out[(first + blk) * f.ntex + i] = texel_fp16<4>(sh.desc[blk], sh.luts, f, x, y);
     }
 }
 
@@ -391,7 +465,7 @@ int device_tables(int bx, int by, const AkvTables** out) {
     return 0;
 }
 
-uint32_t magic(uint32_t d) { return (65536u + d - 1) / d; }
+uint32_t magic(uint32_t d) { return ((1u << 24) + d - 1) / d; }
 
 int check_common(const AkvAttnParams* p, uint32_t* G) {
     if (!p) return AKV_HIP_ERR_NULL;
@@ -401,9 +475,20 @@ int check_common(const AkvAttnParams* p, uint32_t* G) {
     if (g != 1 && g != 2 && g != 3 && g != 4 && g != 8) return AKV_HIP_ERR_SHAPE;
     if (p->batch > 65535 || p->kv_heads > 65535) return AKV_HIP_ERR_SHAPE;
     if (p->tile_tokens == 0) return AKV_HIP_ERR_TILE;
-    if (p->splits != (p->tokens + p->tile_tokens - 1) / p->tile_tokens) return AKV_HIP_ERR_TILE;
+    if (p->splits != (p->tokens + p->tile_tokens - 1) / p->tile_tokens || p->splits > 2147483647u)
+        return AKV_HIP_ERR_TILE;
     *G = g;
     return 0;
+}
+
+Footprint footprint(uint32_t bx, uint32_t by) {
+    Footprint f{};
+    f.bx = int(bx);
+    f.by = int(by);
+    f.ntex = int(bx * by);
+    f.ds = int((1024 + bx / 2) / (bx - 1));
+    f.dt = int((1024 + by / 2) / (by - 1));
+    return f;
 }
 
 int check_astc(const AkvAttnParams* p) {
@@ -412,40 +497,71 @@ int check_astc(const AkvAttnParams* p) {
     if (bx < 4 || by < 4 || bx > 12 || by > 12 || bx * by > uint32_t(akv::kMaxTexels)) return AKV_HIP_ERR_FOOTPRINT;
     const uint32_t texcols = p->layout == AKV_LAYOUT_SCALAR ? p->dim : p->dim / 4;
     if (p->atlas_cols != (texcols + bx - 1) / bx) return AKV_HIP_ERR_SHAPE;
-    const uint32_t cap = p->layout == AKV_LAYOUT_SCALAR ? ChunkCap<1>::blocks : ChunkCap<4>::blocks;
-    if (p->atlas_cols > cap) return AKV_HIP_ERR_SHAPE;
     if (p->tile_tokens % by) return AKV_HIP_ERR_TILE;
     if (uint64_t(p->atlas_rows) * by < p->tokens) return AKV_HIP_ERR_SHAPE;
     return 0;
 }
 
-KernelArgs make_args(const AkvAttnParams* p, uint32_t G) {
-    KernelArgs a{};
-    a.p = *p;
-    a.G = G;
-    const int bx = int(p->block_x ? p->block_x : 4), by = int(p->block_y ? p->block_y : 4);
-    a.ds = (1024 + bx / 2) / (bx - 1);
-    a.dt = (1024 + by / 2) / (by - 1);
-    a.mag_bx = magic(uint32_t(bx));
-    a.mag_by = magic(uint32_t(by));
-    a.mag_cols = magic(p->atlas_cols ? p->atlas_cols : 1);
-    a.qscale = float(1.4426950408889634 / std::sqrt(double(p->dim)));
-    const uint32_t max_tile = uint32_t(kTileElems) / p->dim;
-    a.sub_tokens = max_tile / uint32_t(by) * uint32_t(by);
-    return a;
+// Chunk shape: the most block rows whose blocks fit the header stage and whose
+// tokens, rounded up to whole 16-token tiles, fit the LDS tile; never more
+// than one split. The FP16 control uses whole LDS tiles.
+template <int D, int NCH, bool ASTC>
+int plan_chunks(const AkvAttnParams* p, KernelArgs* a) {
+    using C = Cfg<D, NCH, ASTC>;
+    if (!ASTC) {
+        a->chunk_rows = 0;
+        a->chunk_tokens = C::kVtTok;
+    } else {
+        const uint32_t cols = p->atlas_cols, by = p->block_y;
+        uint32_t r = uint32_t(C::kMaxBlocks) / cols;
+        while (r > 0 && (r * by + 15) / 16 * 16 > uint32_t(C::kVtTok)) --r;
+        if (r == 0) return AKV_HIP_ERR_SHAPE;
+        const uint32_t tile_rows = p->tile_tokens / by;
+        if (tile_rows < r) r = tile_rows;
+        a->chunk_rows = r;
+        a->chunk_tokens = r * by;
+    }
+    if (a->chunk_tokens > p->tile_tokens) a->chunk_tokens = p->tile_tokens;
+    return 0;
 }
 
+int make_args(const AkvAttnParams* p, bool astc, KernelArgs* a) {
+    *a = KernelArgs{};
+    a->p = *p;
+    if (astc) {
+        a->fp = footprint(p->block_x, p->block_y);
+        a->mag_by = magic(p->block_y);
+        a->mag_bx = magic(p->block_x);
+    }
+    a->qscale = float(1.4426950408889634 / std::sqrt(double(p->dim)));
+    const bool scalar = astc && p->layout == AKV_LAYOUT_SCALAR;
+    if (!astc) return p->dim == 64 ? plan_chunks<64, 4, false>(p, a) : plan_chunks<128, 4, false>(p, a);
+    if (p->dim == 64) return scalar ? plan_chunks<64, 1, true>(p, a) : plan_chunks<64, 4, true>(p, a);
+    return scalar ? plan_chunks<128, 1, true>(p, a) : plan_chunks<128, 4, true>(p, a);
+}
+
+struct Ptrs {
+    const float* q;
+    const uint16_t* k;
+    const uint4* vblk;
+    const uint16_t* vh;
+    const uint16_t* vs;
+    const uint16_t* vo;
+    const AkvTables* tab;
+    float* partial;
+    float* stats;
+    uint16_t* dump;
+};
+
 template <int D, int NCH, bool ASTC, bool DUMP>
-hipError_t launch_split_g(const KernelArgs& a, const float* q, const uint16_t* k, const uint4* vblk,
-                          const uint16_t* vh, const uint16_t* vs, const uint16_t* vo, const AkvTables* tab,
-                          float* partial, float* stats, uint16_t* dump, hipStream_t st) {
+hipError_t launch_g(const KernelArgs& a, uint32_t G, const Ptrs& x, hipStream_t st) {
     dim3 grid(a.p.splits, a.p.kv_heads, a.p.batch);
-    auto* s2 = reinterpret_cast<float2*>(stats);
-    switch (a.G) {
-#define AKV_CASE(GG)                                                                                      \
-    case GG:                                                                                              \
-        split_kernel<D, NCH, GG, ASTC, DUMP><<<grid, kThreads, 0, st>>>(a, q, k, vblk, vh, vs, vo, tab,   \
-                                                                         partial, s2, dump);              \
+    auto* s2 = reinterpret_cast<float2*>(x.stats);
+    switch (G) {
+#define AKV_CASE(GG)                                                                                             \
+    case GG:                                                                                                     \
+        attn_kernel<D, NCH, GG, ASTC, DUMP><<<grid, kThreads, 0, st>>>(a, x.q, x.k, x.vblk, x.vh, x.vs, x.vo,   \
+                                                                        x.tab, x.partial, s2, x.dump);          \
         break;
         AKV_CASE(1)
         AKV_CASE(2)
@@ -460,18 +576,45 @@ hipError_t launch_split_g(const KernelArgs& a, const float* q, const uint16_t* k
 }
 
 template <bool ASTC, bool DUMP>
-hipError_t launch_split(const KernelArgs& a, const float* q, const uint16_t* k, const uint4* vblk,
-                        const uint16_t* vh, const uint16_t* vs, const uint16_t* vo, const AkvTables* tab,
-                        float* partial, float* stats, uint16_t* dump, hipStream_t st) {
-    const bool rgba = a.p.layout == AKV_LAYOUT_RGBA;
-    if (a.p.dim == 64)
-        return rgba || !ASTC ? launch_split_g<64, 4, ASTC, DUMP>(a, q, k, vblk, vh, vs, vo, tab, partial, stats, dump, st)
-                             : launch_split_g<64, 1, ASTC, DUMP>(a, q, k, vblk, vh, vs, vo, tab, partial, stats, dump, st);
-    return rgba || !ASTC ? launch_split_g<128, 4, ASTC, DUMP>(a, q, k, vblk, vh, vs, vo, tab, partial, stats, dump, st)
-                         : launch_split_g<128, 1, ASTC, DUMP>(a, q, k, vblk, vh, vs, vo, tab, partial, stats, dump, st);
+hipError_t launch(const KernelArgs& a, uint32_t G, const Ptrs& x, hipStream_t st) {
+    if constexpr (ASTC) {
+        const bool scalar = a.p.layout == AKV_LAYOUT_SCALAR;
+        if (a.p.dim == 64)
+            return scalar ? launch_g<64, 1, true, DUMP>(a, G, x, st) : launch_g<64, 4, true, DUMP>(a, G, x, st);
+        return scalar ? launch_g<128, 1, true, DUMP>(a, G, x, st) : launch_g<128, 4, true, DUMP>(a, G, x, st);
+    } else {
+        if (a.p.dim == 64) return launch_g<64, 4, false, false>(a, G, x, st);
+        return launch_g<128, 4, false, false>(a, G, x, st);
+    }
 }
 
 int as_int(hipError_t e) { return e == hipSuccess ? 0 : int(e); }
+
+hipError_t launch_merge(const AkvAttnParams* p, const float* partial, const float* stats, float* out, hipStream_t st) {
+    const uint64_t groups = uint64_t(p->batch) * p->query_heads;
+    if (groups > 0x7FFFFFFFu) return hipErrorInvalidValue;
+    merge_kernel<<<dim3(uint32_t(groups)), dim3(kThreads), 0, st>>>(p->splits, p->dim, partial,
+                                                                    reinterpret_cast<const float2*>(stats), out);
+    return hipGetLastError();
+}
+
+int run_astc(const AkvAttnParams* p, const float* q, const uint16_t* k, const void* v_blocks, const uint16_t* v_scale,
+             const uint16_t* v_offset, float* partial, float* stats, float* out, bool with_merge, void* stream) {
+    uint32_t G = 0;
+    if (int rc = check_common(p, &G)) return rc;
+    if (int rc = check_astc(p)) return rc;
+    if (!q || !k || !v_blocks || !v_scale || !v_offset || !partial || !stats || (with_merge && !out))
+        return AKV_HIP_ERR_NULL;
+    const AkvTables* tab = nullptr;
+    if (int rc = device_tables(int(p->block_x), int(p->block_y), &tab)) return rc;
+    KernelArgs a;
+    if (int rc = make_args(p, true, &a)) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const Ptrs x{q, k, static_cast<const uint4*>(v_blocks), nullptr, v_scale, v_offset, tab, partial, stats, nullptr};
+    hipError_t e = launch<true, false>(a, G, x, st);
+    if (e == hipSuccess && with_merge) e = launch_merge(p, partial, stats, out, st);
+    return as_int(e);
+}
 
 }  // namespace
 }  // namespace akv_hip
@@ -483,15 +626,7 @@ extern "C" {
 int akv_hip_attention_split(const AkvAttnParams* p, const float* q, const uint16_t* k, const void* v_blocks,
                             const uint16_t* v_scale, const uint16_t* v_offset, float* partial, float* stats,
                             void* stream) {
-    uint32_t G = 0;
-    if (int rc = check_common(p, &G)) return rc;
-    if (int rc = check_astc(p)) return rc;
-    if (!q || !k || !v_blocks || !v_scale || !v_offset || !partial || !stats) return AKV_HIP_ERR_NULL;
-    const AkvTables* tab = nullptr;
-    if (int rc = device_tables(int(p->block_x), int(p->block_y), &tab)) return rc;
-    KernelArgs a = make_args(p, G);
-    return as_int(launch_split<true, false>(a, q, k, static_cast<const uint4*>(v_blocks), nullptr, v_scale, v_offset,
-                                            tab, partial, stats, nullptr, static_cast<hipStream_t>(stream)));
+    return run_astc(p, q, k, v_blocks, v_scale, v_offset, partial, stats, nullptr, false, stream);
 }
 
 int akv_hip_attention_merge(const AkvAttnParams* p, const float* partial, const float* stats, float* out,
@@ -499,17 +634,13 @@ int akv_hip_attention_merge(const AkvAttnParams* p, const float* partial, const 
     uint32_t G = 0;
     if (int rc = check_common(p, &G)) return rc;
     if (!partial || !stats || !out) return AKV_HIP_ERR_NULL;
-    merge_kernel<<<dim3(p->batch * p->query_heads), dim3(p->dim), 0, static_cast<hipStream_t>(stream)>>>(
-        p->splits, p->dim, partial, reinterpret_cast<const float2*>(stats), out);
-    return as_int(hipGetLastError());
+    return as_int(launch_merge(p, partial, stats, out, static_cast<hipStream_t>(stream)));
 }
 
 int akv_hip_decode_attention(const AkvAttnParams* p, const float* q, const uint16_t* k, const void* v_blocks,
                              const uint16_t* v_scale, const uint16_t* v_offset, float* partial, float* stats,
                              float* out, void* stream) {
-    if (!out) return AKV_HIP_ERR_NULL;
-    if (int rc = akv_hip_attention_split(p, q, k, v_blocks, v_scale, v_offset, partial, stats, stream)) return rc;
-    return akv_hip_attention_merge(p, partial, stats, out, stream);
+    return run_astc(p, q, k, v_blocks, v_scale, v_offset, partial, stats, out, true, stream);
 }
 
 int akv_hip_fp16_attention(const AkvAttnParams* p, const float* q, const uint16_t* k, const uint16_t* v,
@@ -517,11 +648,13 @@ int akv_hip_fp16_attention(const AkvAttnParams* p, const float* q, const uint16_
     uint32_t G = 0;
     if (int rc = check_common(p, &G)) return rc;
     if (!q || !k || !v || !partial || !stats || !out) return AKV_HIP_ERR_NULL;
-    KernelArgs a = make_args(p, G);
+    KernelArgs a;
+    if (int rc = make_args(p, false, &a)) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    hipError_t e = launch_split<false, false>(a, q, k, nullptr, v, nullptr, nullptr, nullptr, partial, stats, nullptr, st);
-    if (e != hipSuccess) return int(e);
-    return akv_hip_attention_merge(p, partial, stats, out, stream);
+    const Ptrs x{q, k, nullptr, v, nullptr, nullptr, nullptr, partial, stats, nullptr};
+    hipError_t e = launch<false, false>(a, G, x, st);
+    if (e == hipSuccess) e = launch_merge(p, partial, stats, out, st);
+    return as_int(e);
 }
 
 int akv_hip_decode_values(const AkvAttnParams* p, const void* v_blocks, uint16_t* u, void* stream) {
@@ -531,9 +664,11 @@ int akv_hip_decode_values(const AkvAttnParams* p, const void* v_blocks, uint16_t
     if (!v_blocks || !u) return AKV_HIP_ERR_NULL;
     const AkvTables* tab = nullptr;
     if (int rc = device_tables(int(p->block_x), int(p->block_y), &tab)) return rc;
-    KernelArgs a = make_args(p, G);
-    return as_int(launch_split<true, true>(a, nullptr, nullptr, static_cast<const uint4*>(v_blocks), nullptr, nullptr,
-                                           nullptr, tab, nullptr, nullptr, u, static_cast<hipStream_t>(stream)));
+    KernelArgs a;
+    if (int rc = make_args(p, true, &a)) return rc;
+    const Ptrs x{nullptr, nullptr, static_cast<const uint4*>(v_blocks), nullptr, nullptr, nullptr, tab, nullptr,
+                 nullptr, u};
+    return as_int(launch<true, true>(a, G, x, static_cast<hipStream_t>(stream)));
 }
 
 int akv_hip_decode_blocks(const void* blocks, size_t n, unsigned bx, unsigned by, uint16_t* texels, void* stream) {
@@ -542,12 +677,22 @@ int akv_hip_decode_blocks(const void* blocks, size_t n, unsigned bx, unsigned by
     if (n == 0) return 0;
     const AkvTables* tab = nullptr;
     if (int rc = device_tables(int(bx), int(by), &tab)) return rc;
-    const int ds = int((1024 + bx / 2) / (bx - 1)), dt = int((1024 + by / 2) / (by - 1));
-    const size_t groups = (n + ChunkCap<4>::blocks - 1) / ChunkCap<4>::blocks;
+    const Footprint f = footprint(bx, by);
+    const size_t groups = (n + kThreads - 1) / kThreads;
     if (groups > 0x7FFFFFFF) return AKV_HIP_ERR_SHAPE;
     decode_blocks_kernel<<<dim3(unsigned(groups)), dim3(kThreads), 0, static_cast<hipStream_t>(stream)>>>(
-        static_cast<const uint4*>(blocks), n, int(bx), int(by), ds, dt, tab, reinterpret_cast<uint2*>(texels));
+        static_cast<const uint4*>(blocks), n, f, tab, reinterpret_cast<uint2*>(texels));
     return as_int(hipGetLastError());
+}
+
+int akv_hip_task_tokens(const AkvAttnParams* p, int astc) {
+    uint32_t G = 0;
+    if (int rc = check_common(p, &G)) return rc;
+    if (astc)
+        if (int rc = check_astc(p)) return rc;
+    KernelArgs a;
+    if (int rc = make_args(p, astc != 0, &a)) return rc;
+    return int(a.chunk_tokens);
 }
 
 const char* akv_hip_error_string(int code) {

@@ -200,7 +200,7 @@ def main(argv=None):
     u = gpu.decode_values(dev)
     v16 = (u.float() * dev.scale.float()[..., None] + dev.offset.float()[..., None]).half()
     del u
-    fparams = gpu.fp16_params(a.batch, a.kv_heads, a.query_heads, a.tokens, a.dim, params.tile_tokens)
+    fparams = gpu.fp16_params(a.batch, a.kv_heads, a.query_heads, a.tokens, a.dim)
     fpool = [(kt, v16)] + [(kt.clone(), v16.clone()) for _ in range(max(1, int(np.ceil(
         a.pool_mb * 1e6 / (kt.numel() * 4)))) - 1)]
     fpart = torch.empty((a.batch, a.query_heads, fparams.splits, a.dim), dtype=torch.float32, device="cuda")

@@ -103,6 +103,12 @@ int akv_hip_decode_values(const AkvAttnParams* p, const void* v_blocks, uint16_t
 int akv_hip_decode_blocks(const void* blocks, size_t n, unsigned bx, unsigned by, uint16_t* texels,
                           void* stream);
 
+/* Host-side planning query, no GPU work: tokens per chunk (the whole block
+   rows a workgroup decodes and attends at once; a split of tile_tokens is
+   processed in ceil(tile/chunk) chunks) for these parameters with ASTC V
+   (astc != 0) or for the FP16 control, or a negative AKV_HIP_* code. */
+int akv_hip_task_tokens(const AkvAttnParams* p, int astc);
+
 /* Text for a return code of the functions above. */
 const char* akv_hip_error_string(int code);
 
