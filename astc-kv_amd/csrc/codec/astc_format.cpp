@@ -271,6 +271,7 @@ bool build_tables(int bx, int by, AkvTables* t) {
         t->ise[r] = uint16_t(kIse[r].bits | kIse[r].trit << 8 | kIse[r].quint << 9);
     for (int r = 0; r < 12; ++r)
         for (int v = 0; v < ise_levels(r); ++v) t->weight_unq[r][v] = uint8_t(unquant_weight(r, v));
+    for (int r = 0; r < 12; ++r) t->weight_levels[r] = uint8_t(ise_levels(r));
     for (int r = 0; r < kNumRanges; ++r)
         for (int v = 0; v < ise_levels(r); ++v) t->color_unq[r][v] = uint8_t(unquant_color(r, v));
     for (int pairs = 0; pairs < 10; ++pairs)

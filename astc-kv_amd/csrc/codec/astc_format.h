@@ -30,10 +30,14 @@ inline constexpr uint32_t mode_wbits(uint32_t m) { return (m >> 13) & 127u; }
 inline constexpr uint32_t mode_identity(uint32_t m) { return (m >> 20) & 1u; }
 
 struct AkvTables {
+    // --- leading kLdsTableBytes bytes: the per-block decode tables, which the
+    // --- GPU kernels copy into LDS as one contiguous block.
     uint32_t block_mode[2048];
-    // Partition of each texel for 2, 3 and 4 partitions and every 10-bit seed:
-    // texel i occupies bits 2*(i%16) of word i/16.
-    uint32_t partition[3][1024][4];
+    // Unquantised colour value 0..255 for each range and ISE value.
+    uint8_t color_unq[kNumRanges][256];
+    // Highest colour range whose ISE sequence of 2*pairs values fits in the
+    // available bits, or -1. Index [pairs 1..9][bits 0..127].
+    int8_t color_range[10][128];
     // 8-bit trit block -> five trits, trit j in bits 2j..2j+1.
     uint16_t trit[256];
     // 7-bit quint block -> three quints, quint j in bits 3j..3j+2.
@@ -43,13 +47,18 @@ struct AkvTables {
     uint16_t pad0;
     // Unquantised weight 0..64 for each weight range (0..11) and ISE value.
     uint8_t weight_unq[12][32];
-    // Unquantised colour value 0..255 for each range and ISE value.
-    uint8_t color_unq[kNumRanges][256];
-    // Highest colour range whose ISE sequence of 2*pairs values fits in the
-    // available bits, or -1. Index [pairs 1..9][bits 0..127].
-    int8_t color_range[10][128];
+    // Number of values of each weight range (2, 3, 4, 5, 6, 8, ..., 32).
+    uint8_t weight_levels[12];
+    uint8_t pad1[8];
+    // --- end of the LDS block.
+    // Partition of each texel for 2, 3 and 4 partitions and every 10-bit seed:
+    // texel i occupies bits 2*(i%16) of word i/16.
+    uint32_t partition[3][1024][4];
     uint32_t block_x, block_y;
 };
+
+constexpr size_t kLdsTableBytes = offsetof(AkvTables, partition);
+static_assert(kLdsTableBytes % 16 == 0, "LDS table block must be a whole number of 16-byte copies");
 
 // ISE helpers.
 int ise_bits(int range);        // plain bits per value

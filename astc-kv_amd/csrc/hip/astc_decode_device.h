@@ -1,7 +1,8 @@
 // gfx950 software ASTC LDR decode in two stages that each keep a whole
 // workgroup busy.
 //
-//  1. decode_header: one lane per 16-byte block. Block mode, partitioning,
+//  1. decode_header: one lane per 16-byte block, every lookup table in LDS
+//     except the partition patterns. Block mode, partitioning,
 //     colour endpoint modes, colour integer-sequence (BISE) unpack, endpoint
 //     unquantisation and decode, and the weight BISE unpacked into plain
 //     nb-bit fields (grid order). The result is a 104-byte BlockDesc in LDS.
@@ -28,15 +29,29 @@ namespace akv_hip {
 
 using akv::AkvTables;
 
-// Per-workgroup lookup tables in LDS.
-struct SmallLuts {
+// The per-block decode tables, copied into LDS by every workgroup: the
+// leading akv::kLdsTableBytes bytes of AkvTables, field for field.
+struct alignas(16) LdsTables {
+    uint32_t block_mode[2048];
+    uint8_t color_unq[akv::kNumRanges][256];
+    int8_t color_range[10][128];
     uint16_t trit[256];
     uint16_t quint[128];
     uint16_t ise[akv::kNumRanges];
-    uint8_t levels[12];
-    uint8_t pad[6];
-    uint8_t wunq[12][32];
+    uint16_t pad0;
+    uint8_t weight_unq[12][32];
+    uint8_t weight_levels[12];
+    uint8_t pad1[8];
 };
+static_assert(sizeof(LdsTables) == akv::kLdsTableBytes, "LdsTables mirrors the head of AkvTables");
+static_assert(offsetof(LdsTables, color_unq) == offsetof(AkvTables, color_unq) &&
+                  offsetof(LdsTables, color_range) == offsetof(AkvTables, color_range) &&
+                  offsetof(LdsTables, trit) == offsetof(AkvTables, trit) &&
+                  offsetof(LdsTables, quint) == offsetof(AkvTables, quint) &&
+                  offsetof(LdsTables, ise) == offsetof(AkvTables, ise) &&
+                  offsetof(LdsTables, weight_unq) == offsetof(AkvTables, weight_unq) &&
+                  offsetof(LdsTables, weight_levels) == offsetof(AkvTables, weight_levels),
+              "LdsTables field offsets");
 
 // BlockDesc.info fields (bits 0-3 grid width, 4-7 grid height).
 constexpr uint32_t kInfoDual = 1u << 8;         // bits 9-10: colour component of plane 1
@@ -63,38 +78,39 @@ struct Footprint {
     int bx, by, ntex, ds, dt;   // ds, dt: weight infill steps (1024 + b/2) / (b - 1)
 };
 
-__device__ inline void stage_luts(const AkvTables* __restrict__ tab, SmallLuts& L, int tid, int nthreads) {
-    constexpr uint8_t kLevels[12] = {2, 3, 4, 5, 6, 8, 10, 12, 16, 20, 24, 32};
-    for (int i = tid; i < 256; i += nthreads) L.trit[i] = tab->trit[i];
-    for (int i = tid; i < 128; i += nthreads) L.quint[i] = tab->quint[i];
-    for (int i = tid; i < akv::kNumRanges; i += nthreads) L.ise[i] = tab->ise[i];
-    for (int i = tid; i < 12; i += nthreads) L.levels[i] = kLevels[i];
-    for (int i = tid; i < 12 * 32; i += nthreads) (&L.wunq[0][0])[i] = (&tab->weight_unq[0][0])[i];
+// Copy the decode tables into LDS (16-byte copies; `tab` is 256-byte aligned).
+__device__ inline void stage_tables(const AkvTables* __restrict__ tab, LdsTables& L, int tid, int nthreads) {
+    const uint4* src = reinterpret_cast<const uint4*>(tab);
+    uint4* dst = reinterpret_cast<uint4*>(&L);
+    for (int i = tid; i < int(sizeof(LdsTables) / 16); i += nthreads) dst[i] = src[i];
 }
 
-// Bits [pos, pos+n) of a 128-bit value, 0 < n <= 40; bits past 127 read zero.
-struct Bits128 {
-    uint64_t lo, hi;
-    __device__ inline uint64_t get(int pos, int n) const {
-        uint64_t v;
-        if (pos >= 64) v = hi >> (pos - 64);
-        else if (pos == 0) v = lo;
-        else v = (lo >> pos) | (hi << (64 - pos));
-        return v & ((uint64_t(1) << n) - 1);
-    }
-};
-
-__device__ inline int ise_sequence_bits(int count, int n, bool trit, bool quint) {
-    int b = count * n;
-    if (trit) b += (count * 8 + 4) / 5;
-    if (quint) b += (count * 7 + 2) / 3;
-    return b;
+// Bits [pos, pos + len) of a little-endian bit stream held in LDS dwords
+// (0 <= len < 32; the dword after the one holding bit pos must be readable).
+__device__ inline uint32_t stream_bits(const uint32_t* s, int pos, int len) {
+    const int w = pos >> 5;
+    return __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(s[w + 1], s[w], uint32_t(pos & 31)), 0, uint32_t(len));
 }
 
-// Colour value j of this lane's unpacked colour integers (bytes in LDS,
-// column-major [5][stride] dwords).
-__device__ inline int cval(const uint32_t* cv, int stride, int j) {
-    return int((cv[(j >> 2) * stride] >> (8 * (j & 3))) & 0xFF);
+// As stream_bits, with the bits at or past `end` read as zero (the last group
+// of an integer sequence may be cut short). Branch-free.
+__device__ inline uint32_t stream_bits_until(const uint32_t* s, int pos, int len, int end) {
+    return stream_bits(s, pos, min(max(end - pos, 0), len));
+}
+
+// Up to 40 bits [pos, pos + len) of an LDS bit stream as a 64-bit value,
+// bits at or past `end` zero (reads three dwords).
+__device__ inline uint64_t stream_bits64_until(const uint32_t* s, int pos, int len, int end) {
+    const int w = pos >> 5, sh = pos & 31;
+    const uint32_t lo = __builtin_amdgcn_alignbit(s[w + 1], s[w], uint32_t(sh));
+    const uint32_t hi = __builtin_amdgcn_alignbit(s[w + 2], s[w + 1], uint32_t(sh));
+    const int n = min(max(end - pos, 0), len);
+    const uint64_t v = uint64_t(lo) | (uint64_t(hi) << 32);
+    return n >= 64 ? v : v & ((uint64_t(1) << n) - 1);
+}
+
+__device__ inline uint32_t field64(uint64_t g, int pos, int len) {
+    return uint32_t(g >> pos) & ((1u << len) - 1);
 }
 
 __device__ inline int clamp255(int v) { return v < 0 ? 0 : (v > 255 ? 255 : v); }
@@ -105,11 +121,12 @@ __device__ inline void bit_transfer(int& offset, int& base) {
     if (offset & 0x20) offset -= 0x40;
 }
 
-// Endpoint decode of one partition: 8-bit RGBA pairs. False for HDR modes.
-__device__ inline bool cem_endpoints(int cem, const uint32_t* cv, int stride, int k, int* e0, int* e1) {
+// Endpoint decode of one partition from its unquantised colour values
+// cv[k..]: 8-bit RGBA pairs. False for HDR modes.
+__device__ inline bool cem_endpoints(int cem, const uint8_t* cv, int k, int* e0, int* e1) {
     int v[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = (j < 2 * ((cem >> 2) + 1)) ? cval(cv, stride, k + j) : 0;
+    for (int j = 0; j < 8; ++j) v[j] = (j < 2 * ((cem >> 2) + 1)) ? int(cv[k + j]) : 0;
     switch (cem) {
         case 0:
             e0[0] = e0[1] = e0[2] = v[0]; e0[3] = 255;
@@ -231,70 +248,138 @@ __device__ inline void set_constant(BlockDesc<NCH>& d, uint32_t r, uint32_t g, u
     d.info = kInfoTable | kInfoIdentity | (1u << kInfoLevelsShift);
 }
 
-// Appends nb-bit fields to the five-word weight stream of a BlockDesc.
+// Appends fields (at most 25 bits at a time) to the five-word weight stream
+// of a BlockDesc, low bits first. Branch-free: the current partial word is
+// stored on every put and overwritten once it fills.
 struct FieldWriter {
     uint32_t* out;
-    uint64_t acc;
+    uint32_t cur;
     int bits, words;
-    __device__ inline void put(uint32_t v, int nb) {
-        acc |= uint64_t(v) << bits;
-        bits += nb;
-        if (bits >= 32) {
-            out[words++] = uint32_t(acc);
-            acc >>= 32;
-            bits -= 32;
-        }
+    __device__ inline void put(uint32_t v, int len) {   // v < 2^len, 0 <= len <= 25
+        const uint64_t a = uint64_t(cur) | (uint64_t(v) << bits);
+        const bool full = bits + len >= 32;
+        out[words] = uint32_t(a);
+        cur = full ? uint32_t(a >> 32) : uint32_t(a);
+        bits += len - (full ? 32 : 0);
+        words += full ? 1 : 0;
     }
     __device__ inline void finish() {
-        if (bits > 0) out[words++] = uint32_t(acc);
-        for (; words < 5; ++words) out[words] = 0;
+        out[words] = cur;
+        for (int w = words + 1; w < 5; ++w) out[w] = 0;
     }
 };
 
-// Stage 1: one lane decodes one block into `d`. `cv` is this lane's column of
-// a [5][stride] dword scratch array for the unpacked colour values.
+// Before decode_header runs, a block waits in its own BlockDesc::tab:
+//   tab[0..3]   the 128-bit block, little endian;
+//   tab[4..7]   its partition_words;
+//   tab[8..11]  the block bit-reversed (the weight stream from bit 0), tab[12] = 0.
 template <int NCH>
-__device__ void decode_header(uint4 raw, const AkvTables* __restrict__ tab, const SmallLuts& L, BlockDesc<NCH>& d,
-                              uint32_t* cv, int stride) {
-    const Bits128 b{uint64_t(raw.x) | (uint64_t(raw.y) << 32), uint64_t(raw.z) | (uint64_t(raw.w) << 32)};
+__device__ inline void stash_block(BlockDesc<NCH>& d, uint4 raw, uint4 pw) {
+    uint4* t = reinterpret_cast<uint4*>(d.tab);
+    t[0] = raw;
+    t[1] = pw;
+    t[2] = uint4{__builtin_bitreverse32(raw.w), __builtin_bitreverse32(raw.z), __builtin_bitreverse32(raw.y),
+                 __builtin_bitreverse32(raw.x)};
+    d.tab[12] = 0;
+}
+
+// Decode-path class of a block, 0..kPathKeys-1: blocks of one class take the
+// same branches through decode_header (weight and colour integer-sequence
+// kinds, partition count), so sorting a chunk's blocks by class before the
+// header stage keeps the lanes of a wave on one path. Constant blocks (void
+// extent, reserved or invalid modes) are class kPathKeys - 1.
+constexpr int kPathKeys = 64;
+
+__device__ inline int block_path_key(uint4 raw, const LdsTables& L) {
     const uint32_t mode = raw.x & 0x7FF;
+    const uint32_t md = L.block_mode[mode];
+    const int parts = int((raw.x >> 11) & 3) + 1;
+    if ((mode & 0x1FF) == 0x1FC || !md || (akv::mode_dual(md) && parts == 4)) return kPathKeys - 1;
+    const uint32_t wise = L.ise[akv::mode_range(md)];
+    const int wkind = (wise >> 8) & 3;   // 0 plain, 1 trit, 2 quint
+    // Colour range as decode_header derives it.
+    int below = 128 - int(akv::mode_wbits(md)) - (akv::mode_dual(md) ? 2 : 0);
+    uint32_t cems;
+    if (parts == 1) {
+        cems = (raw.x >> 13) & 15;
+    } else {
+        const uint32_t sel = (raw.x >> 23) & 0x3F;
+        if ((sel & 3) == 0) {
+            cems = (sel >> 2) * 0x1111u;
+        } else {
+            below -= 3 * parts - 4;
+            // Only the classes matter for the value count: class + "up" bit.
+            const int base_class = int(sel & 3) - 1;
+            cems = 0;
+            for (int p = 0; p < parts; ++p) cems |= uint32_t((base_class + ((sel >> (2 + p)) & 1)) << 2) << (4 * p);
+        }
+    }
+    int pairs = 0;
+    for (int p = 0; p < parts; ++p) pairs += int((cems >> (4 * p)) & 15) / 4 + 1;
+    const int avail = below - (parts == 1 ? 17 : 29);
+    const int crange = (pairs <= 9 && avail > 0) ? int(L.color_range[pairs][min(avail, 127)]) : -1;
+    if (crange < akv::kRange6) return kPathKeys - 1;
+    const int ckind = (L.ise[crange] >> 8) & 3;
+    return wkind | (ckind << 2) | ((parts - 1) << 4);
+}
+
+// The partition-pattern words a block selects (any 128-bit value selects an
+// in-range entry; blocks with one partition, void-extent and error blocks
+// ignore it). This is the header stage's only global-memory read, so callers
+// issue it early, ahead of other loads.
+__device__ inline uint4 partition_words(uint4 raw, const AkvTables* __restrict__ tab) {
+    const int parts = int((raw.x >> 11) & 3) + 1;
+    if (parts == 1) return uint4{0, 0, 0, 0};
+    return *reinterpret_cast<const uint4*>(tab->partition[parts - 2][(raw.x >> 13) & 0x3FF]);
+}
+
+// Stage 1: one lane decodes the block stashed in `d` (stash_block) into `d`.
+// `cv` is this lane's 20-byte scratch for the unquantised colour values.
+// Every table read is from LDS.
+template <int NCH>
+__device__ __attribute__((always_inline)) inline void decode_header(const LdsTables& L, BlockDesc<NCH>& d,
+                                                                   uint8_t* cv) {
+    const uint32_t* blk = d.tab;        // block bits
+    const uint32_t* rev = d.tab + 8;    // weight stream
+    const uint32_t w0 = blk[0];
+    const uint32_t mode = w0 & 0x7FF;
     if ((mode & 0x1FF) == 0x1FC) {
         // Void extent: LDR constant colour (UNORM16 RGBA in bits 64..127).
-        uint32_t s0 = uint32_t(b.get(12, 13)), s1 = uint32_t(b.get(25, 13));
-        uint32_t t0 = uint32_t(b.get(38, 13)), t1 = uint32_t(b.get(51, 13));
-        bool unbounded = (s0 & s1 & t0 & t1) == 0x1FFF;
-        bool hdr = (raw.x >> 9) & 1;
+        const uint32_t s0 = stream_bits(blk, 12, 13), s1 = stream_bits(blk, 25, 13);
+        const uint32_t t0 = stream_bits(blk, 38, 13), t1 = stream_bits(blk, 51, 13);
+        const uint32_t c01 = blk[2], c23 = blk[3];
+        const bool unbounded = (s0 & s1 & t0 & t1) == 0x1FFF;
+        const bool hdr = (w0 >> 9) & 1;
         if (hdr || (!unbounded && (s0 >= s1 || t0 >= t1))) set_constant(d, 0xFFFF, 0, 0xFFFF, 0xFFFF);
-        else set_constant(d, raw.z & 0xFFFF, raw.z >> 16, raw.w & 0xFFFF, raw.w >> 16);
+        else set_constant(d, c01 & 0xFFFF, c01 >> 16, c23 & 0xFFFF, c23 >> 16);
         return;
     }
-    const uint32_t md = tab->block_mode[mode];
-    const int parts = int((raw.x >> 11) & 3) + 1;
+    const uint32_t md = L.block_mode[mode];
+    const int parts = int((w0 >> 11) & 3) + 1;
     if (!md || (akv::mode_dual(md) && parts == 4)) {
         set_constant(d, 0xFFFF, 0, 0xFFFF, 0xFFFF);
         return;
     }
     const int wbits = int(akv::mode_wbits(md));
     int below = 128 - wbits;
-    int color_start = 17, seed = 0;
+    int color_start = 17;
     uint32_t cems;  // 4 bits per partition
     if (parts == 1) {
-        cems = (raw.x >> 13) & 15;
+        cems = (w0 >> 13) & 15;
     } else {
-        seed = int((raw.x >> 13) & 0x3FF);
         color_start = 29;
-        uint32_t sel = (raw.x >> 23) & 0x3F;
+        uint32_t sel = (w0 >> 23) & 0x3F;
         if ((sel & 3) == 0) {
             cems = (sel >> 2) * 0x1111u;
         } else {
-            int extra = 3 * parts - 4;
+            const int extra = 3 * parts - 4;
             below -= extra;
-            sel |= uint32_t(b.get(below, extra)) << 6;
-            int base_class = int(sel & 3) - 1;
+            sel |= stream_bits(blk, below, extra) << 6;
+            const int base_class = int(sel & 3) - 1;
             cems = 0;
             for (int p = 0; p < parts; ++p) {
-                int up = (sel >> (2 + p)) & 1;
-                int low = (sel >> (2 + parts + 2 * p)) & 3;
+                const int up = (sel >> (2 + p)) & 1;
+                const int low = (sel >> (2 + parts + 2 * p)) & 3;
                 cems |= uint32_t(((base_class + up) << 2) | low) << (4 * p);
             }
         }
@@ -303,148 +388,138 @@ __device__ void decode_header(uint4 raw, const AkvTables* __restrict__ tab, cons
     uint32_t ccs = 0;
     if (dual) {
         below -= 2;
-        ccs = uint32_t(b.get(below, 2));
+        ccs = stream_bits(blk, below, 2);
     }
     int pairs = 0;
     for (int p = 0; p < parts; ++p) pairs += int((cems >> (4 * p)) & 15) / 4 + 1;
     const int avail = below - color_start;
-    const int crange = (pairs <= 9 && avail > 0) ? int(tab->color_range[pairs][min(avail, 127)]) : -1;
+    const int crange = (pairs <= 9 && avail > 0) ? int(L.color_range[pairs][min(avail, 127)]) : -1;
     if (crange < akv::kRange6) {
         set_constant(d, 0xFFFF, 0, 0xFFFF, 0xFFFF);
         return;
     }
-    // Partition pattern, issued before the colour unpack needs its own loads.
-    uint4 pw = uint4{0, 0, 0, 0};
-    if (parts > 1) pw = *reinterpret_cast<const uint4*>(tab->partition[parts - 2][seed]);
+    const uint4 pw = *reinterpret_cast<const uint4*>(d.tab + 4);
 
-    // Colour integer sequence -> unquantised bytes, four per scratch dword.
+    // Colour integer sequence -> unquantised colour bytes. The loops are
+    // unrolled and branch-free so that their LDS reads issue together: values
+    // and groups past the sequence read bits of this block's own record
+    // (garbage, at most 210 bits in) and their bytes are never used.
     {
         const int nv = 2 * pairs;
         const uint32_t ise = L.ise[crange];
         const int n = int(ise & 0xFF);
-        const bool trit = (ise >> 8) & 1, quint = (ise >> 9) & 1;
-        const int end = color_start + ise_sequence_bits(nv, n, trit, quint);
-        const uint64_t mask = (uint64_t(1) << n) - 1;
-        const uint8_t* unq = tab->color_unq[crange];
-        uint32_t packed[5] = {0, 0, 0, 0, 0};
-        if (trit) {
-            const int gb = 5 * n + 8;
+        const uint8_t* unq = L.color_unq[crange];
+        if (ise & 0x100) {
+            const int end = color_start + nv * n + (nv * 8 + 4) / 5;
+            const int moff[5] = {0, n + 2, 2 * n + 4, 3 * n + 5, 4 * n + 7};
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                if (5 * g < nv) {
-                    int pos = color_start + g * gb;
-                    uint64_t G = b.get(pos, min(gb, end - pos));
-                    uint32_t T = uint32_t((G >> n) & 3) | uint32_t((G >> (2 * n + 2)) & 3) << 2 |
-                                 uint32_t((G >> (3 * n + 4)) & 1) << 4 | uint32_t((G >> (4 * n + 5)) & 3) << 5 |
-                                 uint32_t((G >> (5 * n + 7)) & 1) << 7;
-                    uint32_t dig = L.trit[T];
-                    const int moff[5] = {0, n + 2, 2 * n + 4, 3 * n + 5, 4 * n + 7};
+                const int pos = color_start + g * (5 * n + 8);
+                const uint64_t G = stream_bits64_until(blk, pos, 5 * n + 8, end);
+                const uint32_t T = field64(G, n, 2) | field64(G, 2 * n + 2, 2) << 2 | field64(G, 3 * n + 4, 1) << 4 |
+                                   field64(G, 4 * n + 5, 2) << 5 | field64(G, 5 * n + 7, 1) << 7;
+                const uint32_t dig = L.trit[T];
 #pragma unroll
-                    for (int j = 0; j < 5; ++j) {
-                        const int idx = 5 * g + j;
-                        if (idx < 20 && idx < nv) {
-                            uint32_t v = (((dig >> (2 * j)) & 3) << n) | uint32_t((G >> moff[j]) & mask);
-                            packed[idx >> 2] |= uint32_t(unq[v]) << (8 * (idx & 3));
-                        }
-                    }
-                }
+                for (int j = 0; j < 5; ++j)
+                    if (5 * g + j < 18) cv[5 * g + j] = unq[(((dig >> (2 * j)) & 3) << n) | field64(G, moff[j], n)];
             }
-        } else if (quint) {
-            const int gb = 3 * n + 7;
+        } else if (ise & 0x200) {
+            const int end = color_start + nv * n + (nv * 7 + 2) / 3;
+            const int moff[3] = {0, n + 3, 2 * n + 5};
 #pragma unroll
             for (int g = 0; g < 6; ++g) {
-                if (3 * g < nv) {
-                    int pos = color_start + g * gb;
-                    uint64_t G = b.get(pos, min(gb, end - pos));
-                    uint32_t Q = uint32_t((G >> n) & 7) | uint32_t((G >> (2 * n + 3)) & 3) << 3 |
-                                 uint32_t((G >> (3 * n + 5)) & 3) << 5;
-                    uint32_t dig = L.quint[Q];
-                    const int moff[3] = {0, n + 3, 2 * n + 5};
+                const int pos = color_start + g * (3 * n + 7);
+                const uint32_t G = stream_bits_until(blk, pos, 3 * n + 7, end);   // at most 22 bits
+                const uint32_t Q = __builtin_amdgcn_ubfe(G, n, 3) | __builtin_amdgcn_ubfe(G, 2 * n + 3, 2) << 3 |
+                                   __builtin_amdgcn_ubfe(G, 3 * n + 5, 2) << 5;
+                const uint32_t dig = L.quint[Q];
 #pragma unroll
-                    for (int j = 0; j < 3; ++j) {
-                        const int idx = 3 * g + j;
-                        if (idx < nv) {
-                            uint32_t v = (((dig >> (3 * j)) & 7) << n) | uint32_t((G >> moff[j]) & mask);
-                            packed[idx >> 2] |= uint32_t(unq[v]) << (8 * (idx & 3));
-                        }
-                    }
-                }
+                for (int j = 0; j < 3; ++j)
+                    cv[3 * g + j] = unq[(((dig >> (3 * j)) & 7) << n) | __builtin_amdgcn_ubfe(G, moff[j], n)];
             }
         } else {
 #pragma unroll
-            for (int idx = 0; idx < 18; ++idx)
-                if (idx < nv) packed[idx >> 2] |= uint32_t(unq[b.get(color_start + idx * n, n)]) << (8 * (idx & 3));
+            for (int j = 0; j < 18; ++j) cv[j] = unq[stream_bits(blk, color_start + j * n, n)];
         }
-#pragma unroll
-        for (int i = 0; i < 5; ++i) cv[i * stride] = packed[i];
     }
 
-    // Weights: the BISE stream runs from bit 127 downwards, so in the
-    // bit-reversed block it starts at bit 0. Unpack it to nb-bit fields.
+    // Weights: the integer sequence runs from bit 127 downwards, so in the
+    // bit-reversed block it starts at bit 0. Unpacked to nb-bit fields, one
+    // appended chunk per group (a group is at most 23 bits). Unrolled and
+    // branch-free like the colour loops: at most 96 weight bits make at most
+    // 12 trit groups or 14 quint groups.
     const int wrange = int(akv::mode_range(md));
     const uint32_t wise = L.ise[wrange];
     const int n = int(wise & 0xFF);
-    const bool wtrit = (wise >> 8) & 1, wquint = (wise >> 9) & 1;
     const int nw = int(akv::mode_gw(md) * akv::mode_gh(md)) << (dual ? 1 : 0);
-    const uint32_t rev[5] = {__builtin_bitreverse32(raw.w), __builtin_bitreverse32(raw.z),
-                             __builtin_bitreverse32(raw.y), __builtin_bitreverse32(raw.x), 0u};
     int nb = n;
-    if (!wtrit && !wquint) {
-        // Plain binary fields are nb-bit fields of the reversed stream already;
-        // fields past the weight count are never read.
-#pragma unroll
-        for (int i = 0; i < 5; ++i) d.qw[i] = rev[i];
-    } else {
-        FieldWriter fw{d.qw, 0, 0, 0};
-        if (wtrit) {
+    if (wise & 0x300) {
+        FieldWriter fw{d.qw, 0u, 0, 0};
+        if (wise & 0x100) {
             nb = n + 2;
-            const int gb = 5 * n + 8;
-            for (int g = 0, pos = 0; 5 * g < nw; ++g, pos += gb) {
-                const int w = pos >> 5;
-                uint32_t G = __builtin_amdgcn_alignbit(rev[w + 1], rev[w], uint32_t(pos & 31));
-                const int len = min(gb, wbits - pos);
-                if (len < 32) G &= (1u << len) - 1;
+            const int moff[5] = {0, n + 2, 2 * n + 4, 3 * n + 5, 4 * n + 7};
+#pragma unroll
+            for (int g = 0; g < 12; ++g) {
+                const int pos = g * (5 * n + 8);
+                const uint32_t G = stream_bits_until(rev, pos, 5 * n + 8, wbits);
                 const uint32_t T = __builtin_amdgcn_ubfe(G, n, 2) | __builtin_amdgcn_ubfe(G, 2 * n + 2, 2) << 2 |
                                    __builtin_amdgcn_ubfe(G, 3 * n + 4, 1) << 4 |
                                    __builtin_amdgcn_ubfe(G, 4 * n + 5, 2) << 5 |
                                    __builtin_amdgcn_ubfe(G, 5 * n + 7, 1) << 7;
-                const uint32_t dig = L.trit[T];
-                const int cnt = min(5, nw - 5 * g);
-                for (int j = 0; j < cnt; ++j) {
-                    const int moff = j * n + int((0x75420u >> (4 * j)) & 15);
-                    fw.put((((dig >> (2 * j)) & 3) << n) | __builtin_amdgcn_ubfe(G, moff, n), nb);
+                const uint32_t dig = L.trit[T];   // five 2-bit trits: the fields themselves when n == 0
+                uint32_t chunk = dig;
+                if (n > 0) {
+                    chunk = 0;
+#pragma unroll
+                    for (int j = 0; j < 5; ++j)
+                        chunk |= ((((dig >> (2 * j)) & 3) << n) | __builtin_amdgcn_ubfe(G, moff[j], n)) << (j * nb);
                 }
+                const int len = min(max(nw - 5 * g, 0), 5) * nb;
+                fw.put(__builtin_amdgcn_ubfe(chunk, 0, len), len);
             }
         } else {
             nb = n + 3;
-            const int gb = 3 * n + 7;
-            for (int g = 0, pos = 0; 3 * g < nw; ++g, pos += gb) {
-                const int w = pos >> 5;
-                uint32_t G = __builtin_amdgcn_alignbit(rev[w + 1], rev[w], uint32_t(pos & 31));
-                const int len = min(gb, wbits - pos);
-                if (len < 32) G &= (1u << len) - 1;
+            const int moff[3] = {0, n + 3, 2 * n + 5};
+#pragma unroll
+            for (int g = 0; g < 14; ++g) {
+                const int pos = g * (3 * n + 7);
+                const uint32_t G = stream_bits_until(rev, pos, 3 * n + 7, wbits);
                 const uint32_t Q = __builtin_amdgcn_ubfe(G, n, 3) | __builtin_amdgcn_ubfe(G, 2 * n + 3, 2) << 3 |
                                    __builtin_amdgcn_ubfe(G, 3 * n + 5, 2) << 5;
-                const uint32_t dig = L.quint[Q];
-                const int cnt = min(3, nw - 3 * g);
-                for (int j = 0; j < cnt; ++j) {
-                    const int moff = j * n + int((0x530u >> (4 * j)) & 15);
-                    fw.put((((dig >> (3 * j)) & 7) << n) | __builtin_amdgcn_ubfe(G, moff, n), nb);
+                const uint32_t dig = L.quint[Q];  // three 3-bit quints: the fields themselves when n == 0
+                uint32_t chunk = dig;
+                if (n > 0) {
+                    chunk = 0;
+#pragma unroll
+                    for (int j = 0; j < 3; ++j)
+                        chunk |= ((((dig >> (3 * j)) & 7) << n) | __builtin_amdgcn_ubfe(G, moff[j], n)) << (j * nb);
                 }
+                const int len = min(max(nw - 3 * g, 0), 3) * nb;
+                fw.put(__builtin_amdgcn_ubfe(chunk, 0, len), len);
             }
         }
         fw.finish();
+    } else {
+        // Plain binary fields are nb-bit fields of the reversed stream already;
+        // fields past the weight count are never read.
+        const uint4 r4 = *reinterpret_cast<const uint4*>(rev);
+        d.qw[0] = r4.x;
+        d.qw[1] = r4.y;
+        d.qw[2] = r4.z;
+        d.qw[3] = r4.w;
+        d.qw[4] = 0;
     }
 
-    // Endpoints per partition -> endpoint pairs, or the texel table.
-    const int levels = L.levels[wrange];
+    // Endpoints per partition -> endpoint pairs, or the texel table. (The
+    // table and endpoint pairs overwrite the stash, which is no longer read.)
+    const int levels = L.weight_levels[wrange];
     const bool identity = akv::mode_identity(md);
     const bool table = identity && !dual && parts * levels <= BlockDesc<NCH>::kTabEntries;
     for (int p = 0, k = 0; p < parts; ++p) {
         const int cem = int((cems >> (4 * p)) & 15);
         int e0[4], e1[4];
         uint32_t ep[NCH];
-        if (cem_endpoints(cem, cv, stride, k, e0, e1)) {
+        if (cem_endpoints(cem, cv, k, e0, e1)) {
 #pragma unroll
             for (int ch = 0; ch < NCH; ++ch) ep[ch] = uint32_t(e0[ch] * 257) | (uint32_t(e1[ch] * 257) << 16);
         } else {
@@ -454,8 +529,12 @@ __device__ void decode_header(uint4 raw, const AkvTables* __restrict__ tab, cons
         }
         k += 2 * ((cem >> 2) + 1);
         if (table) {
-            for (int q = 0; q < levels; ++q)
-                put_entry<NCH>(d.tab, p * levels + q, ep, weight_pair(L.wunq[wrange][q]));
+            // Entries past this partition's row are rewritten by the next
+            // partition or unused; none lies past the table.
+#pragma unroll
+            for (int q = 0; q < BlockDesc<NCH>::kTabEntries; ++q)
+                if (p * levels + q < BlockDesc<NCH>::kTabEntries)
+                    put_entry<NCH>(d.tab, p * levels + q, ep, weight_pair(L.weight_unq[wrange][q]));
         } else {
 #pragma unroll
             for (int ch = 0; ch < NCH; ++ch) d.ep[p][ch] = ep[ch];
@@ -478,15 +557,16 @@ __device__ inline uint32_t field_at(const BlockDesc<NCH>& d, uint32_t nb, int id
 }
 
 // Unquantised, infilled weight of texel (x, y) on plane `plane` (compute path).
+// bx: footprint width; ds, dt: the footprint's infill steps.
 template <int NCH>
-__device__ inline int texel_weight(const BlockDesc<NCH>& d, const SmallLuts& L, const Footprint& f, uint32_t info,
+__device__ inline int texel_weight(const BlockDesc<NCH>& d, const LdsTables& L, int bx, int ds, int dt, uint32_t info,
                                    int x, int y, int plane) {
     const uint32_t nb = (info >> kInfoNbShift) & 7;
-    const uint8_t* unq = L.wunq[(info >> kInfoRangeShift) & 15];
+    const uint8_t* unq = L.weight_unq[(info >> kInfoRangeShift) & 15];
     const int sh = (info & kInfoDual) ? 1 : 0;
-    if (info & kInfoIdentity) return unq[field_at(d, nb, ((y * f.bx + x) << sh) + plane)];
+    if (info & kInfoIdentity) return unq[field_at(d, nb, ((y * bx + x) << sh) + plane)];
     const int gw = int(info & 15), gh = int((info >> 4) & 15);
-    const int gs = (f.ds * x * (gw - 1) + 32) >> 6, gt = (f.dt * y * (gh - 1) + 32) >> 6;
+    const int gs = (ds * x * (gw - 1) + 32) >> 6, gt = (dt * y * (gh - 1) + 32) >> 6;
     const int fs = gs & 15, ft = gt & 15, base = (gs >> 4) + (gt >> 4) * gw;
     const int f11 = (fs * ft + 8) >> 4, f01 = fs - f11, f10 = ft - f11, f00 = 16 - fs - ft + f11;
     // Taps with a zero factor may lie outside the grid: read the base tap instead.
@@ -496,10 +576,29 @@ __device__ inline int texel_weight(const BlockDesc<NCH>& d, const SmallLuts& L, 
            4;
 }
 
+// Stage 2, compute path (blocks that are not a table): kept out of line, so
+// the table path that nearly every block takes stays small where it is
+// inlined. `p` is the texel's partition; scalars are passed by value so that
+// nothing of the caller's has to live in memory for the call.
+template <int NCH>
+__device__ __attribute__((noinline)) uint2 texel_compute(const BlockDesc<NCH>& d, const LdsTables& L, int bx, int ds,
+                                                         int dt, int x, int y, int p) {
+    const uint32_t info = d.info;
+    const uint32_t wp0 = weight_pair(texel_weight(d, L, bx, ds, dt, info, x, y, 0));
+    const uint32_t wp1 =
+        (info & kInfoDual) ? weight_pair(texel_weight(d, L, bx, ds, dt, info, x, y, 1)) : wp0;
+    const int ccs = (info & kInfoDual) ? int((info >> 9) & 3) : 4;
+    uint32_t C[NCH];
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) C[ch] = interp_c(d.ep[p][ch], ch == ccs ? wp1 : wp0);
+    if constexpr (NCH == 4) return uint2{pack_fp16_rtz(C[0], C[1]), pack_fp16_rtz(C[2], C[3])};
+    else return uint2{pack_fp16_rtz(C[0], 0) & 0xFFFFu, 0u};
+}
+
 // Stage 2: the FP16 values of texel (x, y) of a block (NCH == 4:
 // {R | G << 16, B | A << 16}; NCH == 1: R in the low half of .x).
 template <int NCH>
-__device__ inline uint2 texel_fp16(const BlockDesc<NCH>& d, const SmallLuts& L, const Footprint& f, int x, int y) {
+__device__ inline uint2 texel_fp16(const BlockDesc<NCH>& d, const LdsTables& L, Footprint f, int x, int y) {
     const uint32_t info = d.info;
     const int i = y * f.bx + x;
     const int p = int(__builtin_amdgcn_ubfe(d.part[i >> 4], 2 * (i & 15), 2));
@@ -509,14 +608,7 @@ __device__ inline uint2 texel_fp16(const BlockDesc<NCH>& d, const SmallLuts& L, 
         if constexpr (NCH == 4) return *reinterpret_cast<const uint2*>(&d.tab[2 * entry]);
         else return uint2{reinterpret_cast<const uint16_t*>(d.tab)[entry], 0u};
     }
-    const uint32_t wp0 = weight_pair(texel_weight(d, L, f, info, x, y, 0));
-    const uint32_t wp1 = (info & kInfoDual) ? weight_pair(texel_weight(d, L, f, info, x, y, 1)) : wp0;
-    const int ccs = (info & kInfoDual) ? int((info >> 9) & 3) : 4;
-    uint32_t C[NCH];
-#pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) C[ch] = interp_c(d.ep[p][ch], ch == ccs ? wp1 : wp0);
-    if constexpr (NCH == 4) return uint2{pack_fp16_rtz(C[0], C[1]), pack_fp16_rtz(C[2], C[3])};
-    else return uint2{pack_fp16_rtz(C[0], 0) & 0xFFFFu, 0u};
+    return texel_compute<NCH>(d, L, f.bx, f.ds, f.dt, x, y, p);
 }
 
 }  // namespace akv_hip

@@ -7,22 +7,25 @@
 // of split states).
 //
 // Split kernel schedule. One 256-lane workgroup per (sequence, kv head,
-// split). A split is processed in chunks of whole block rows (at most 144
-// blocks and 240 tokens for head dim 64). Per chunk:
-//   1. header stage, one lane per block: BlockDesc records in LDS (the
-//      chunk's blocks were loaded one chunk ahead);
-//   2. the chunk's K rows are loaded into registers in the MFMA operand
-//      layout (16-byte loads) while the texel stage runs, and the next
-//      chunk's blocks are requested;
-//   3. texel stage, one lane per pair of tokens: u (the exact FP16 values
-//      astcenc returns) channel-major into the LDS tile vt;
-//   4. each wave takes every fourth 16-token tile: S^T = K.Q^T and O += V^T.P
-//      on the matrix cores (v_mfma_f32_16x16x16_f16, q and p split into fp16
-//      high and low parts so the products keep ~22 bits), the G query heads
-//      padded to the 16 MFMA columns; online softmax per head with the per-token
-//      V scale folded into p and the offset term accumulated separately.
-// At the end the four wave states are combined into the split's state.
-// A second kernel merges the splits.
+// split); a split is processed in chunks of whole block rows (at most 144
+// blocks and 256 tokens for head dim 64, 128 for head dim 128). Per chunk:
+//   1. the partition-pattern words of the chunk's blocks are requested first
+//      (the blocks themselves were loaded one chunk ahead), then the chunk's
+//      K rows (16-byte loads, in the MFMA operand layout) and the per-token V
+//      scale/offset, then the next chunk's blocks;
+//   2. header stage, one lane per block: BlockDesc records in LDS;
+//   3. each wave takes every fourth 16-token tile of the chunk. A lane decodes
+//      the texels of its MFMA operand directly: 4 consecutive tokens of one
+//      texel column (RGBA: 4 channels each, so one decode feeds 4 MFMA row
+//      blocks; the row blocks therefore hold channels 4x + j, x = texel
+//      column, and the output is un-permuted at the end). Then S^T = K.Q^T and
+//      O += V^T.P on the matrix cores (v_mfma_f32_16x16x16_f16; q and p are
+//      split into fp16 high and low parts so the products keep ~22 bits), the
+//      G query heads padded to the 16 MFMA columns, with an online softmax per
+//      head, the per-token V scale folded into p and the offset term summed
+//      separately.
+// At the end the four wave states are combined into the split's state; the
+// merge kernel combines the splits.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -39,29 +42,32 @@ namespace akv_hip {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
+constexpr int kMaxG = 8;   // query heads per kv head
+#ifndef AKV_ASTC_WAVES
+#define AKV_ASTC_WAVES 3   // waves per SIMD the split kernel is register-limited to
+#endif
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-template <int D, int NCH, bool ASTC>
+template <int D, int NCH>
 struct Cfg {
-    static constexpr int kMaxBlocks = ASTC ? 144 : 1;                // blocks per chunk
-    static constexpr int kVtTok = ASTC ? (D == 64 ? 240 : 112) : (D == 64 ? 256 : 128);
-    static constexpr int kVtStride = kVtTok + 4;                     // odd multiple of 8 bytes per row
-    static constexpr int kMaxTiles = kVtTok / 16;                    // 16-token MFMA tiles per chunk
-    static constexpr int kWaveTiles = (kMaxTiles + kWaves - 1) / kWaves;
-    static constexpr int kRowLoads = D / 32;                         // 16-byte row loads per lane per tile
+    static constexpr int kMaxBlocks = 144;                       // blocks per chunk (header stage)
+    static constexpr int kMaxTok = D == 64 ? 256 : 128;          // tokens per chunk
+    static constexpr int kMaxTiles = kMaxTok / 16;
+    static constexpr int kWaveTiles = kMaxTiles / kWaves;        // tiles per wave per chunk
+    static constexpr int kRowLoads = D / 32;                     // K: 16-byte loads per lane per tile
     static constexpr int kKSteps = D / 16;
     static constexpr int kMBlocks = D / 16;
-    static_assert((kVtStride / 4) % 2 == 1, "vt rows must be an odd multiple of 8 bytes");
+    static constexpr int kColGroups = NCH == 4 ? D / 64 : D / 16; // texel columns per lane
 };
 
 struct KernelArgs {
     AkvAttnParams p;
     Footprint fp;
-    uint32_t chunk_rows, chunk_tokens;   // block rows / tokens per full chunk
-    uint32_t mag_by, mag_bx;             // ceil(2^24 / divisor)
-    float qscale;                        // log2(e) / sqrt(dim)
+    uint32_t chunk_tokens;   // tokens per full chunk (whole block rows for ASTC V)
+    uint32_t mag_by, mag_bx; // ceil(2^24 / divisor)
+    float qscale;            // log2(e) / sqrt(dim)
 };
 
 // a / d with magic = ceil(2^24 / d): exact when a * d < 2^24 (the error term
@@ -69,306 +75,405 @@ struct KernelArgs {
 __device__ inline uint32_t fdiv(uint32_t a, uint32_t magic) { return (a * magic) >> 24; }
 __device__ inline float half_to_float(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
 
-// Order this wave's LDS accesses (a wave's LDS operations complete in order).
-__device__ inline void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
+// Channel held by row `row` of MFMA row block `mb` of P.V. RGBA texels (and the
+// FP16 control) feed row blocks 4k + j with channel j of texel column
+// 16k + row; scalar texels feed row block k with texel column 16k + row.
+template <int NCH>
+__device__ inline int pv_channel(int mb, int row) {
+    if constexpr (NCH == 4) return 64 * (mb >> 2) + 4 * row + (mb & 3);
+    else return 16 * mb + row;
 }
 
-template <int D, int NCH, bool ASTC>
-struct Shared {
-    using C = Cfg<D, NCH, ASTC>;
-    union {
-        _Float16 vt[D][C::kVtStride];   // u (or fp16 V), channel-major
-        float comb[kWaves][D][16];      // final per-wave accumulators
-    } u;
-    BlockDesc<NCH> desc[C::kMaxBlocks];
-    uint32_t cv[5][C::kMaxBlocks];      // colour values of the header stage
-    uint32_t so[2][C::kVtTok];          // per-token V scale | offset << 16 (fp16), two chunks
-    SmallLuts luts;
-    float wm[kWaves][16], wl[kWaves][16], wo[kWaves][16];
-};
-
-// 16-byte rows of one wave's tiles in the MFMA A-operand layout: lane holds
-// token 16 * tile + lane % 16, dims 32 * L + 8 * (lane / 16) .. + 7. Tokens at
-// or past ntok read as zero.
-template <int D, int NCH, bool ASTC>
-__device__ inline void load_rows(uint4* r, const uint16_t* __restrict__ seq, int c0, int ntok, int wave, int lane) {
-    using C = Cfg<D, NCH, ASTC>;
-    const int n16 = lane & 15, g = lane >> 4;
+// Q as the B operand of Q.K^T, split into fp16 high and low parts. k-step ks
+// covers dims 32*(ks/2) + 8*g + 4*(ks%2) + j, matching the K row loads.
+template <int D, int G>
+__device__ inline void load_q(const float* __restrict__ qrow, float qscale, int n16, int g, half4* qhi, half4* qlo) {
 #pragma unroll
-    for (int j = 0; j < C::kWaveTiles; ++j)
-#pragma unroll
-        for (int L = 0; L < C::kRowLoads; ++L) {
-            const int tok = 16 * (wave + kWaves * j) + n16;
-            r[j * C::kRowLoads + L] =
-                tok < ntok ? *reinterpret_cast<const uint4*>(seq + size_t(c0 + tok) * D + 32 * L + 8 * g)
-                           : uint4{0, 0, 0, 0};
-        }
-}
-
-// The blocks of the chunk starting at block row `row0` (one per lane).
-template <int D, int NCH>
-__device__ inline uint4 load_block(const KernelArgs& a, const uint4* __restrict__ bseq, int row0, int nrows, int tid) {
-    const int nblk = nrows * int(a.p.atlas_cols);
-    return tid < nblk ? bseq[size_t(row0) * a.p.atlas_cols + tid] : uint4{0, 0, 0, 0};
-}
-
-// Texel stage: one lane per (texel column, token pair) of the chunk; u into vt.
-// Token columns from ntok up to the tile edge are zeroed.
-template <int D, int NCH, bool ASTC>
-__device__ inline void decode_texels(Shared<D, NCH, ASTC>& sh, const KernelArgs& a, int ntok, int tid) {
-    const Footprint& f = a.fp;
-    const int cols = int(a.p.atlas_cols);
-    constexpr int TC = NCH == 1 ? D : D / 4;   // texel columns holding channels
-    const int pairs = 8 * ((ntok + 15) >> 4);
-    const uint32_t mag = (0x1000000u + uint32_t(pairs) - 1) / uint32_t(pairs);
-    for (int it = tid; it < pairs * TC; it += kThreads) {
-        const int x = int(fdiv(uint32_t(it), mag));
-        const int t = 2 * (it - x * pairs);
-        const int bc = int(fdiv(uint32_t(x), a.mag_bx)), xx = x - bc * f.bx;
-        uint2 v[2];
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            v[k] = uint2{0, 0};
-            if (t + k < ntok) {
-                const int r = int(fdiv(uint32_t(t + k), a.mag_by)), y = t + k - r * f.by;
-                v[k] = texel_fp16<NCH>(sh.desc[r * cols + bc], sh.luts, f, xx, y);
-            }
-        }
-        if constexpr (NCH == 1) {
-            *reinterpret_cast<uint32_t*>(&sh.u.vt[x][t]) = v[0].x | (v[1].x << 16);
-        } else {
-            *reinterpret_cast<uint32_t*>(&sh.u.vt[4 * x + 0][t]) = __builtin_amdgcn_perm(v[1].x, v[0].x, 0x05040100u);
-            *reinterpret_cast<uint32_t*>(&sh.u.vt[4 * x + 1][t]) = __builtin_amdgcn_perm(v[1].x, v[0].x, 0x07060302u);
-            *reinterpret_cast<uint32_t*>(&sh.u.vt[4 * x + 2][t]) = __builtin_amdgcn_perm(v[1].y, v[0].y, 0x05040100u);
-            *reinterpret_cast<uint32_t*>(&sh.u.vt[4 * x + 3][t]) = __builtin_amdgcn_perm(v[1].y, v[0].y, 0x07060302u);
-        }
-    }
-}
-
-// FP16 control: transpose this wave's V rows (in registers) into its vt columns.
-template <int D, int NCH, bool ASTC>
-__device__ inline void stage_fp16_rows(Shared<D, NCH, ASTC>& sh, const uint4* v, int wave, int lane) {
-    using C = Cfg<D, NCH, ASTC>;
-    const int n16 = lane & 15, g = lane >> 4;
-#pragma unroll
-    for (int j = 0; j < C::kWaveTiles; ++j)
-#pragma unroll
-        for (int L = 0; L < C::kRowLoads; ++L) {
-            const uint4 x = v[j * C::kRowLoads + L];
-            const uint32_t w[4] = {x.x, x.y, x.z, x.w};
-            const int tok = 16 * (wave + kWaves * j) + n16, c0 = 32 * L + 8 * g;
-            if (tok < C::kVtTok) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    sh.u.vt[c0 + 2 * i][tok] = __builtin_bit_cast(_Float16, uint16_t(w[i]));
-                    sh.u.vt[c0 + 2 * i + 1][tok] = __builtin_bit_cast(_Float16, uint16_t(w[i] >> 16));
-                }
-            }
-        }
-}
-
-// --- the split kernel --------------------------------------------------------
-
-template <int D, int NCH, int G, bool ASTC, bool DUMP>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void attn_kernel(
-    KernelArgs a, const float* __restrict__ q, const uint16_t* __restrict__ k, const uint4* __restrict__ vblk,
-    const uint16_t* __restrict__ vh, const uint16_t* __restrict__ vscale, const uint16_t* __restrict__ voffset,
-    const AkvTables* __restrict__ tab, float* __restrict__ partial, float2* __restrict__ stats,
-    uint16_t* __restrict__ dump) {
-    using C = Cfg<D, NCH, ASTC>;
-    __shared__ Shared<D, NCH, ASTC> sh;
-    const AkvAttnParams& p = a.p;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int n16 = lane & 15, g = lane >> 4;
-    const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
-    const int T = int(p.tokens);
-    const int split_begin = split * int(p.tile_tokens);
-    const int split_end = min(split_begin + int(p.tile_tokens), T);
-    const int CT = int(a.chunk_tokens);
-
-    const size_t seq_kv = size_t(b) * p.kv_heads + kh;
-    const uint16_t* kseq = DUMP ? nullptr : k + seq_kv * p.tokens * D;
-    const uint16_t* vseq = ASTC ? nullptr : vh + seq_kv * p.tokens * D;
-    const uint4* bseq = ASTC ? vblk + seq_kv * p.atlas_rows * p.atlas_cols : nullptr;
-    const uint16_t* sseq = (ASTC && !DUMP) ? vscale + seq_kv * p.tokens : nullptr;
-    const uint16_t* oseq = (ASTC && !DUMP) ? voffset + seq_kv * p.tokens : nullptr;
-
-    uint4 raw = uint4{0, 0, 0, 0};
-    if constexpr (ASTC) {
-        const int rows0 = (min(CT, split_end - split_begin) + int(p.block_y) - 1) / int(p.block_y);
-        raw = load_block<D, NCH>(a, bseq, split_begin / int(p.block_y), rows0, tid);
-        stage_luts(tab, sh.luts, tid, kThreads);
-    }
-
-    // Q as the B operand of Q.K^T, split into fp16 high and low parts. k-step
-    // ks covers dims 32*(ks/2) + 8*g + 4*(ks%2) + j, matching the K row loads.
-    half4 qhi[C::kKSteps], qlo[C::kKSteps];
-#pragma unroll
-    for (int ks = 0; ks < C::kKSteps; ++ks)
+    for (int ks = 0; ks < D / 16; ++ks)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            float v = 0.0f;
-            if (!DUMP && n16 < G)
-                v = q[(size_t(b) * p.query_heads + size_t(kh) * G + n16) * D + 32 * (ks / 2) + 8 * g + 4 * (ks % 2) +
-                      j] *
-                    a.qscale;
+            const float v = n16 < G ? qrow[size_t(n16) * D + 32 * (ks / 2) + 8 * g + 4 * (ks % 2) + j] * qscale : 0.0f;
             const _Float16 hi = _Float16(v);
             qhi[ks][j] = hi;
             qlo[ks][j] = _Float16(v - float(hi));
         }
+}
 
-    float m_run = -INFINITY, l_run = 0.0f, off_run = 0.0f;
-    floatx4 o[C::kMBlocks];
+// K rows of one 16-token tile in the MFMA A-operand layout: lane holds token
+// t0 + lane % 16, dims 32 * L + 8 * (lane / 16) .. + 7; tokens at or past ntok
+// read as zero.
+template <int D>
+__device__ inline void load_k_tile(uint4* r, const uint16_t* __restrict__ seq, int t0, int ntok, int lane) {
+    const int tok = t0 + (lane & 15), g = lane >> 4;
 #pragma unroll
-    for (int mb = 0; mb < C::kMBlocks; ++mb) o[mb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    if constexpr (ASTC) __syncthreads();   // LUTs staged
+    for (int L = 0; L < D / 32; ++L)
+        r[L] = tok < ntok ? *reinterpret_cast<const uint4*>(seq + size_t(tok) * D + 32 * L + 8 * g) : uint4{0, 0, 0, 0};
+}
 
-    int buf = 0;
-    for (int c0 = split_begin; c0 < split_end; c0 += CT, buf ^= 1) {
-        const int ntok = min(CT, split_end - c0);
-        const int ntiles = (ntok + 15) >> 4;
-        uint4 kreg[C::kWaveTiles * C::kRowLoads];
-        uint4 vreg[ASTC ? 1 : C::kWaveTiles * C::kRowLoads];
-        if constexpr (ASTC) {
-            // Scale/offset of the chunk's tokens (consumed after the next barrier).
-            uint32_t so = 0;
-            if (!DUMP && tid < ntok) so = uint32_t(sseq[c0 + tid]) | (uint32_t(oseq[c0 + tid]) << 16);
-            // 1. Block headers.
-            const int nblk = ((ntok + int(p.block_y) - 1) / int(p.block_y)) * int(p.atlas_cols);
-            if (tid < nblk) decode_header<NCH>(raw, tab, sh.luts, sh.desc[tid], &sh.cv[0][tid], C::kMaxBlocks);
-            // 2. This chunk's K rows, then the next chunk's blocks.
-            if constexpr (!DUMP) load_rows<D, NCH, ASTC>(kreg, kseq, c0, ntok, wave, lane);
-            const int cn = c0 + CT;
-            if (cn < split_end) {
-                const int rows = (min(CT, split_end - cn) + int(p.block_y) - 1) / int(p.block_y);
-                raw = load_block<D, NCH>(a, bseq, cn / int(p.block_y), rows, tid);
-            }
-            if (!DUMP && tid < ntok) sh.so[buf][tid] = so;
-            __syncthreads();
-            // 3. Texels.
-            decode_texels<D, NCH, ASTC>(sh, a, ntok, tid);
-            __syncthreads();
-        } else {
-            load_rows<D, NCH, ASTC>(kreg, kseq, c0, ntok, wave, lane);
-            load_rows<D, NCH, ASTC>(vreg, vseq, c0, ntok, wave, lane);
-            stage_fp16_rows<D, NCH, ASTC>(sh, vreg, wave, lane);
-            wave_sync();
-        }
-        if constexpr (DUMP) {
-            uint16_t* dst = dump + (seq_kv * p.tokens + c0) * D;
-            for (int i = tid; i < ntok * D; i += kThreads) {
-                const int t = i / D, c = i - t * D;
-                dst[i] = __builtin_bit_cast(uint16_t, sh.u.vt[c][t]);
-            }
-            __syncthreads();
-            continue;
-        }
-
-        // 4. Scores of this wave's tiles.
-        floatx4 s[C::kWaveTiles];
-        float mt = -INFINITY;
+// One tile of attention for one wave: scores from the K rows, online softmax
+// update, and O += V^T P with the V operands va (one half4 per row block).
+// `valid` = tokens of the tile that exist; so4 = per-token (scale | offset<<16)
+// of this lane's four score rows (AFFINE only).
+template <int D, bool AFFINE>
+__device__ inline void attend_tile(const uint4* kr, const half4* qhi, const half4* qlo, const half4* va, uint4 so4,
+                                   int valid, int g, float& m_run, float& l_run, float& off_run, floatx4* o) {
+    floatx4 s = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < C::kWaveTiles; ++j) {
-            const int tt = wave + kWaves * j;
-            s[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (tt >= ntiles) continue;
-#pragma unroll
-            for (int ks = 0; ks < C::kKSteps; ++ks) {
-                const uint4 kk = kreg[j * C::kRowLoads + ks / 2];
-                const half4 ka = __builtin_bit_cast(half4, (ks & 1) ? uint2{kk.z, kk.w} : uint2{kk.x, kk.y});
-                s[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(ka, qhi[ks], s[j], 0, 0, 0);
-                s[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(ka, qlo[ks], s[j], 0, 0, 0);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (16 * tt + 4 * g + i >= ntok) s[j][i] = -INFINITY;
-                mt = fmaxf(mt, s[j][i]);
-            }
-        }
-        if (wave < ntiles) {
-            mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-            mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-            const float m_new = fmaxf(m_run, mt);
-            const float alpha = exp2f(m_run - m_new);
-            m_run = m_new;
-            l_run *= alpha;
-            off_run *= alpha;
-#pragma unroll
-            for (int mb = 0; mb < C::kMBlocks; ++mb) o[mb] *= alpha;
-#pragma unroll
-            for (int j = 0; j < C::kWaveTiles; ++j) {
-                const int tt = wave + kWaves * j;
-                if (tt >= ntiles) break;
-                uint4 so4 = uint4{0x3C00u, 0, 0x3C00u, 0};   // FP16 control: scale 1, offset 0
-                if constexpr (ASTC) so4 = *reinterpret_cast<const uint4*>(&sh.so[buf][16 * tt + 4 * g]);
-                const uint32_t sov[4] = {so4.x, so4.y, so4.z, so4.w};
-                half4 phi, plo;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float pr = exp2f(s[j][i] - m_new);
-                    l_run += pr;
-                    float pv = pr;
-                    if constexpr (ASTC) {
-                        pv = pr * half_to_float(uint16_t(sov[i]));
-                        off_run = fmaf(pr, half_to_float(uint16_t(sov[i] >> 16)), off_run);
-                    }
-                    const _Float16 h = _Float16(pv);
-                    phi[i] = h;
-                    plo[i] = _Float16(pv - float(h));
-                }
-#pragma unroll
-                for (int mb = 0; mb < C::kMBlocks; ++mb) {
-                    const half4 va = *reinterpret_cast<const half4*>(&sh.u.vt[16 * mb + n16][16 * tt + 4 * g]);
-                    o[mb] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, phi, o[mb], 0, 0, 0);
-                    o[mb] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, plo, o[mb], 0, 0, 0);
-                }
-            }
-        }
-        if constexpr (!ASTC) wave_sync();   // this wave's vt columns are rewritten next chunk
+    for (int ks = 0; ks < D / 16; ++ks) {
+        const uint4 kk = kr[ks / 2];
+        const half4 ka = __builtin_bit_cast(half4, (ks & 1) ? uint2{kk.z, kk.w} : uint2{kk.x, kk.y});
+        s = __builtin_amdgcn_mfma_f32_16x16x16f16(ka, qhi[ks], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_16x16x16f16(ka, qlo[ks], s, 0, 0, 0);
     }
-    if constexpr (DUMP) return;
+    float mt = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (4 * g + i >= valid) s[i] = -INFINITY;
+        mt = fmaxf(mt, s[i]);
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float m_new = fmaxf(m_run, mt);   // finite: token 0 of the tile exists
+    const float alpha = exp2f(m_run - m_new);
+    m_run = m_new;
+    const uint32_t sov[4] = {so4.x, so4.y, so4.z, so4.w};
+    float psum = 0.0f, poff = 0.0f;
+    half4 phi, plo;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float pr = exp2f(s[i] - m_new);
+        psum += pr;
+        float pv = pr;
+        if constexpr (AFFINE) {
+            pv = pr * half_to_float(uint16_t(sov[i]));
+            poff = fmaf(pr, half_to_float(uint16_t(sov[i] >> 16)), poff);
+        }
+        const _Float16 h = _Float16(pv);
+        phi[i] = h;
+        plo[i] = _Float16(pv - float(h));
+    }
+    l_run = fmaf(l_run, alpha, psum);
+    off_run = fmaf(off_run, alpha, poff);
+#pragma unroll
+    for (int mb = 0; mb < D / 16; ++mb) {
+        o[mb] *= alpha;
+        o[mb] = __builtin_amdgcn_mfma_f32_16x16x16f16(va[mb], phi, o[mb], 0, 0, 0);
+        o[mb] = __builtin_amdgcn_mfma_f32_16x16x16f16(va[mb], plo, o[mb], 0, 0, 0);
+    }
+}
 
-    // Wave state: sums over the four lane groups; accumulators to LDS.
+struct WaveStats {
+    float wm[kWaves][16], wl[kWaves][16], wo[kWaves][16];
+};
+
+// Combine the four waves' states into this split's state (partial, stats).
+// comb: [kWaves][D][kMaxG] floats in LDS, free for this use.
+template <int D, int NCH, int G>
+__device__ inline void combine_waves(float* comb, WaveStats& ws, const floatx4* o, float m_run, float l_run,
+                                     float off_run, float* __restrict__ partial, float2* __restrict__ stats,
+                                     size_t qh0, int S, int split) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n16 = lane & 15, g = lane >> 4;
     l_run += __shfl_xor(l_run, 16, 64);
     l_run += __shfl_xor(l_run, 32, 64);
     off_run += __shfl_xor(off_run, 16, 64);
     off_run += __shfl_xor(off_run, 32, 64);
-    __syncthreads();   // every wave is done with vt
+    if (n16 < G) {
 #pragma unroll
-    for (int mb = 0; mb < C::kMBlocks; ++mb)
+        for (int mb = 0; mb < D / 16; ++mb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sh.u.comb[wave][16 * mb + 4 * g + i][n16] = o[mb][i];
+            for (int i = 0; i < 4; ++i) comb[(wave * D + pv_channel<NCH>(mb, 4 * g + i)) * kMaxG + n16] = o[mb][i];
+    }
     if (g == 0) {
-        sh.wm[wave][n16] = m_run;
-        sh.wl[wave][n16] = l_run;
-        sh.wo[wave][n16] = off_run;
+        ws.wm[wave][n16] = m_run;
+        ws.wl[wave][n16] = l_run;
+        ws.wo[wave][n16] = off_run;
     }
     __syncthreads();
-
-    // Combine the four waves -> this split's state.
-    const int S = int(p.splits);
     for (int i = tid; i < G * D; i += kThreads) {
         const int h = i / D, c = i - h * D;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sh.wm[w][h]);
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ws.wm[w][h]);
         float acc = 0.0f, l = 0.0f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
-            const float e = sh.wm[w][h] == -INFINITY ? 0.0f : exp2f(sh.wm[w][h] - M);
-            acc = fmaf(e, sh.u.comb[w][c][h] + sh.wo[w][h], acc);
-            l = fmaf(e, sh.wl[w][h], l);
+            const float e = ws.wm[w][h] == -INFINITY ? 0.0f : exp2f(ws.wm[w][h] - M);
+            acc = fmaf(e, comb[(w * D + c) * kMaxG + h] + ws.wo[w][h], acc);
+            l = fmaf(e, ws.wl[w][h], l);
         }
-        const size_t qh = size_t(b) * p.query_heads + size_t(kh) * G + h;
+        const size_t qh = qh0 + h;
         partial[(qh * S + split) * D + c] = acc;
         if (c == 0) stats[qh * S + split] = float2{M * 0.69314718055994531f, l};
     }
 }
 
-// Merge: one workgroup per (sequence, query head); wave w takes splits
-// w, w + 4, ...; lane = channel (and channel + 64 for dim 128).
+// --- ASTC split kernel -------------------------------------------------------
+
+template <int D, int NCH>
+struct AstcShared {
+    using C = Cfg<D, NCH>;
+    LdsTables tabs;
+    union {
+        struct {
+            BlockDesc<NCH> desc[C::kMaxBlocks];
+            uint8_t cv[C::kMaxBlocks][20];   // colour values of the header stage, per lane
+        } h;
+        float comb[kWaves * D * kMaxG];      // final per-wave accumulators
+    } u;
+    uint32_t so[C::kMaxTok];                 // per-token V scale | offset << 16 (fp16)
+    uint32_t key_count[kPathKeys];           // blocks per decode-path class (zero between chunks)
+    uint32_t key_base[kPathKeys];            // first sorted position of each class
+    uint8_t order[C::kMaxBlocks];            // blocks sorted by decode-path class
+    WaveStats ws;
+};
+
+// The chunk's blocks (one per lane) and their partition-pattern words.
+__device__ inline uint4 load_block(const uint4* __restrict__ bseq, uint32_t cols, int row0, int nblk, int tid) {
+    return tid < nblk ? bseq[size_t(row0) * cols + tid] : uint4{0, 0, 0, 0};
+}
+
+template <int D, int NCH, int G, bool DUMP>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_ASTC_WAVES))) void astc_attn_kernel(KernelArgs a, const float* __restrict__ q,
+                                                             const uint16_t* __restrict__ k,
+                                                             const uint4* __restrict__ vblk,
+                                                             const uint16_t* __restrict__ vscale,
+                                                             const uint16_t* __restrict__ voffset,
+                                                             const AkvTables* __restrict__ tab,
+                                                             float* __restrict__ partial, float2* __restrict__ stats,
+                                                             uint16_t* __restrict__ dump) {
+    using C = Cfg<D, NCH>;
+    __shared__ AstcShared<D, NCH> sh;
+    const AkvAttnParams& p = a.p;
+    const Footprint f = a.fp;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int n16 = lane & 15, g = lane >> 4;
+    const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+    const int split_begin = split * int(p.tile_tokens);
+    const int split_end = min(split_begin + int(p.tile_tokens), int(p.tokens));
+    const int CT = int(a.chunk_tokens), by = f.by;
+    const uint32_t cols = p.atlas_cols;
+
+    const size_t seq_kv = size_t(b) * p.kv_heads + kh;
+    const uint16_t* kseq = DUMP ? nullptr : k + seq_kv * p.tokens * D;
+    const uint4* bseq = vblk + seq_kv * p.atlas_rows * cols;
+    const uint16_t* sseq = DUMP ? nullptr : vscale + seq_kv * p.tokens;
+    const uint16_t* oseq = DUMP ? nullptr : voffset + seq_kv * p.tokens;
+
+    auto chunk_blocks = [&](int c0) { return int((min(CT, split_end - c0) + by - 1) / by * cols); };
+    uint4 raw = load_block(bseq, cols, split_begin / by, chunk_blocks(split_begin), tid);
+    stage_tables(tab, sh.tabs, tid, kThreads);
+    if (tid < kPathKeys) sh.key_count[tid] = 0;
+
+    half4 qhi[C::kKSteps], qlo[C::kKSteps];
+    if constexpr (!DUMP) load_q<D, G>(q + (size_t(b) * p.query_heads + size_t(kh) * G) * D, a.qscale, n16, g, qhi, qlo);
+
+    // This lane's texel columns: x = n16 + 16 * kc -> block column and x in block.
+    int bcol[C::kColGroups], xin[C::kColGroups];
+#pragma unroll
+    for (int kc = 0; kc < C::kColGroups; ++kc) {
+        const int x = n16 + 16 * kc;
+        bcol[kc] = int(fdiv(uint32_t(x), a.mag_bx));
+        xin[kc] = x - bcol[kc] * f.bx;
+    }
+
+    float m_run = -INFINITY, l_run = 0.0f, off_run = 0.0f;
+    floatx4 o[C::kMBlocks];
+#pragma unroll
+    for (int mb = 0; mb < C::kMBlocks; ++mb) o[mb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int c0 = split_begin; c0 < split_end; c0 += CT) {
+        const int ntok = min(CT, split_end - c0);
+        const int ntiles = (ntok + 15) >> 4;
+        const int nblk = chunk_blocks(c0);
+        // 1. Loads, in the order they are needed.
+        const uint4 pw = tid < nblk ? partition_words(raw, tab) : uint4{0, 0, 0, 0};
+        uint4 kcur[C::kRowLoads];
+        if constexpr (!DUMP) load_k_tile<D>(kcur, kseq + size_t(c0) * D, 16 * wave, ntok, lane);
+        uint32_t so = 0;
+        if (!DUMP && tid < ntok) so = uint32_t(sseq[c0 + tid]) | (uint32_t(oseq[c0 + tid]) << 16);
+        const uint4 raw_now = raw;
+        if (c0 + CT < split_end) raw = load_block(bseq, cols, (c0 + CT) / by, chunk_blocks(c0 + CT), tid);
+        // 2. Block headers, with the blocks sorted by decode-path class so that
+        // the lanes of a wave take the same branches. Each block's raw bits and
+        // pattern words wait in its own descriptor slot; the lane that decodes
+        // a block reads them from there and overwrites that slot.
+        int key = 0, rank = 0;
+        if (tid < nblk) {
+            key = block_path_key(raw_now, sh.tabs);
+            stash_block(sh.u.h.desc[tid], raw_now, pw);
+            rank = int(atomicAdd(&sh.key_count[key], 1u));
+        }
+        // Tokens past the chunk up to the tile edge get scale = offset = 0.
+        if (!DUMP && tid < 16 * ntiles) sh.so[tid] = so;
+        __syncthreads();
+        if (wave == 0) {   // exclusive scan of the class counts (kPathKeys == 64 lanes)
+            const uint32_t c = sh.key_count[lane];
+            uint32_t incl = c;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const uint32_t t = __shfl_up(incl, d, 64);
+                if (lane >= d) incl += t;
+            }
+            sh.key_base[lane] = incl - c;
+            sh.key_count[lane] = 0;
+        }
+        __syncthreads();
+        if (tid < nblk) sh.order[sh.key_base[key] + rank] = uint8_t(tid);
+        __syncthreads();
+        if (tid < nblk) decode_header<NCH>(sh.tabs, sh.u.h.desc[sh.order[tid]], sh.u.h.cv[tid]);
+        __syncthreads();
+        // 3. This wave's tiles (every fourth): K rows of the next one are
+        // requested first, then texels straight into MFMA operands, then attention.
+#pragma unroll 1
+        for (int t0 = 16 * wave; t0 < ntok; t0 += 16 * kWaves) {
+            uint4 knext[C::kRowLoads];
+            if constexpr (!DUMP) load_k_tile<D>(knext, kseq + size_t(c0) * D, t0 + 16 * kWaves, ntok, lane);
+            const int tq = t0 + 4 * g;   // this lane's 4 tokens: tq .. tq + 3
+            int r = int(fdiv(uint32_t(tq), a.mag_by)), y = tq - r * by;
+            uint2 tx[4][C::kColGroups];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int kc = 0; kc < C::kColGroups; ++kc)
+                    tx[i][kc] = tq + i < ntok ? texel_fp16<NCH>(sh.u.h.desc[r * int(cols) + bcol[kc]], sh.tabs, f,
+                                                                xin[kc], y)
+                                              : uint2{0, 0};
+                if (++y == by) {
+                    y = 0;
+                    ++r;
+                }
+            }
+            if constexpr (DUMP) {
+                uint16_t* dst = dump + (seq_kv * p.tokens + c0) * D;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (tq + i >= ntok) break;
+#pragma unroll
+                    for (int kc = 0; kc < C::kColGroups; ++kc) {
+                        const int x = n16 + 16 * kc;
+                        if constexpr (NCH == 4) *reinterpret_cast<uint2*>(dst + size_t(tq + i) * D + 4 * x) = tx[i][kc];
+                        else dst[size_t(tq + i) * D + x] = uint16_t(tx[i][kc].x);
+                    }
+                }
+                continue;
+            }
+            half4 va[C::kMBlocks];
+#pragma unroll
+            for (int kc = 0; kc < C::kColGroups; ++kc) {
+                if constexpr (NCH == 4) {
+                    const uint32_t sel[2] = {0x05040100u, 0x07060302u};
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+                        const uint32_t s = sel[jj & 1];
+                        const uint32_t lo = jj < 2 ? __builtin_amdgcn_perm(tx[1][kc].x, tx[0][kc].x, s)
+                                                   : __builtin_amdgcn_perm(tx[1][kc].y, tx[0][kc].y, s);
+                        const uint32_t hi = jj < 2 ? __builtin_amdgcn_perm(tx[3][kc].x, tx[2][kc].x, s)
+                                                   : __builtin_amdgcn_perm(tx[3][kc].y, tx[2][kc].y, s);
+                        va[4 * kc + jj] = __builtin_bit_cast(half4, uint2{lo, hi});
+                    }
+                } else {
+                    va[kc] = __builtin_bit_cast(half4, uint2{tx[0][kc].x | (tx[1][kc].x << 16),
+                                                             tx[2][kc].x | (tx[3][kc].x << 16)});
+                }
+            }
+            const uint4 so4 = *reinterpret_cast<const uint4*>(&sh.so[tq]);
+            attend_tile<D, true>(kcur, qhi, qlo, va, so4, ntok - t0, g, m_run, l_run, off_run, o);
+#pragma unroll
+            for (int L = 0; L < C::kRowLoads; ++L) kcur[L] = knext[L];
+        }
+        __syncthreads();   // descriptors and so are rewritten by the next chunk
+    }
+    if constexpr (DUMP) return;
+    combine_waves<D, NCH, G>(sh.u.comb, sh.ws, o, m_run, l_run, off_run, partial, stats,
+                             size_t(b) * p.query_heads + size_t(kh) * G, int(p.splits), split);
+}
+
+// --- FP16-K/V control ----------------------------------------------------------
+
+template <int D>
+struct Fp16Shared {
+    float comb[kWaves * D * kMaxG];
+    WaveStats ws;
+};
+
+// Same tiling, V rows loaded straight into the P.V operand (RGBA-style channel
+// order: lane n16 reads channels 4x .. 4x+3 of texel-column-like group
+// x = n16 + 16k, 8 bytes per token, so 16 lanes read one 128-byte row piece).
+template <int D, int G>
+__global__ __launch_bounds__(kThreads) void fp16_attn_kernel(KernelArgs a, const float* __restrict__ q,
+                                                             const uint16_t* __restrict__ k,
+                                                             const uint16_t* __restrict__ v,
+                                                             float* __restrict__ partial,
+                                                             float2* __restrict__ stats) {
+    using C = Cfg<D, 4>;
+    __shared__ Fp16Shared<D> sh;
+    const AkvAttnParams& p = a.p;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int n16 = lane & 15, g = lane >> 4;
+    const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+    const int split_begin = split * int(p.tile_tokens);
+    const int split_end = min(split_begin + int(p.tile_tokens), int(p.tokens));
+    const int CT = int(a.chunk_tokens);
+    const size_t seq_kv = size_t(b) * p.kv_heads + kh;
+    const uint16_t* kseq = k + seq_kv * p.tokens * D;
+    const uint16_t* vseq = v + seq_kv * p.tokens * D;
+
+    half4 qhi[C::kKSteps], qlo[C::kKSteps];
+    load_q<D, G>(q + (size_t(b) * p.query_heads + size_t(kh) * G) * D, a.qscale, n16, g, qhi, qlo);
+    float m_run = -INFINITY, l_run = 0.0f, off_run = 0.0f;
+    floatx4 o[C::kMBlocks];
+#pragma unroll
+    for (int mb = 0; mb < C::kMBlocks; ++mb) o[mb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int c0 = split_begin; c0 < split_end; c0 += CT) {
+        const int ntok = min(CT, split_end - c0);
+        uint4 kreg[C::kWaveTiles * C::kRowLoads];
+        uint2 vreg[C::kWaveTiles][4][D / 64];
+#pragma unroll
+        for (int j = 0; j < C::kWaveTiles; ++j) {
+            const int t0 = 16 * (wave + kWaves * j);
+            load_k_tile<D>(kreg + j * C::kRowLoads, kseq + size_t(c0) * D, t0, ntok, lane);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int kc = 0; kc < D / 64; ++kc) {
+                    const int t = t0 + 4 * g + i;
+                    vreg[j][i][kc] = t < ntok ? *reinterpret_cast<const uint2*>(vseq + size_t(c0 + t) * D +
+                                                                                 4 * (n16 + 16 * kc))
+                                              : uint2{0, 0};
+                }
+        }
+#pragma unroll
+        for (int j = 0; j < C::kWaveTiles; ++j) {
+            const int t0 = 16 * (wave + kWaves * j);
+            if (t0 >= ntok) break;
+            half4 va[C::kMBlocks];
+#pragma unroll
+            for (int kc = 0; kc < D / 64; ++kc) {
+                const uint32_t sel[2] = {0x05040100u, 0x07060302u};
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const uint32_t s = sel[jj & 1];
+                    const uint32_t lo = jj < 2 ? __builtin_amdgcn_perm(vreg[j][1][kc].x, vreg[j][0][kc].x, s)
+                                               : __builtin_amdgcn_perm(vreg[j][1][kc].y, vreg[j][0][kc].y, s);
+                    const uint32_t hi = jj < 2 ? __builtin_amdgcn_perm(vreg[j][3][kc].x, vreg[j][2][kc].x, s)
+                                               : __builtin_amdgcn_perm(vreg[j][3][kc].y, vreg[j][2][kc].y, s);
+                    va[4 * kc + jj] = __builtin_bit_cast(half4, uint2{lo, hi});
+                }
+            }
+            attend_tile<D, false>(kreg + j * C::kRowLoads, qhi, qlo, va, uint4{0, 0, 0, 0}, ntok - t0, g, m_run,
+                                  l_run, off_run, o);
+        }
+    }
+    __syncthreads();
+    combine_waves<D, 4, G>(sh.comb, sh.ws, o, m_run, l_run, off_run, partial, stats,
+                           size_t(b) * p.query_heads + size_t(kh) * G, int(p.splits), split);
+}
+
+// --- merge ---------------------------------------------------------------------
+
+// One workgroup per (sequence, query head); wave w takes splits w, w + 4, ...;
+// lane = channel (and channel + 64 for dim 128).
 __global__ __launch_bounds__(kThreads) void merge_kernel(uint32_t splits, uint32_t dim,
                                                          const float* __restrict__ partial,
                                                          const float2* __restrict__ stats, float* __restrict__ out) {
@@ -406,28 +511,35 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(uint32_t splits, uint32
     }
 }
 
-// Standalone block decode: 256 blocks per workgroup -> FP16 RGBA texels.
+// --- standalone block decode -------------------------------------------------------
+
 struct BlocksShared {
-    SmallLuts luts;
+    LdsTables tabs;
     BlockDesc<4> desc[kThreads];
-    uint32_t cv[5][kThreads];
+    uint8_t cv[kThreads][20];
 };
 
+// 256 blocks per workgroup -> FP16 RGBA texels [n][by][bx][4].
 __global__ __launch_bounds__(kThreads) void decode_blocks_kernel(const uint4* __restrict__ blocks, size_t n,
                                                                  Footprint f, const AkvTables* __restrict__ tab,
                                                                  uint2* __restrict__ out) {
     __shared__ BlocksShared sh;
     const int tid = threadIdx.x;
-    stage_luts(tab, sh.luts, tid, kThreads);
-    __syncthreads();
     const size_t first = size_t(blockIdx.x) * kThreads;
     const int nblk = int(min(size_t(kThreads), n - first));
-    if (tid < nblk) decode_header<4>(blocks[first + tid], tab, sh.luts, sh.desc[tid], &sh.cv[0][tid], kThreads);
+    const uint4 raw = tid < nblk ? blocks[first + tid] : uint4{0, 0, 0, 0};
+    const uint4 pw = tid < nblk ? partition_words(raw, tab) : uint4{0, 0, 0, 0};
+    stage_tables(tab, sh.tabs, tid, kThreads);
+    __syncthreads();
+    if (tid < nblk) {
+        stash_block(sh.desc[tid], raw, pw);
+        decode_header<4>(sh.tabs, sh.desc[tid], sh.cv[tid]);
+    }
     __syncthreads();
     for (int it = tid; it < nblk * f.ntex; it += kThreads) {
         const int blk = it / f.ntex, i = it - blk * f.ntex;
         const int y = i / f.bx, x = i - y * f.bx;
-        out[(first + blk) * f.ntex + i] = texel_fp16<4>(sh.desc[blk], sh.luts, f, x, y);
+        out[(first + blk) * f.ntex + i] = texel_fp16<4>(sh.desc[blk], sh.tabs, f, x, y);
     }
 }
 
@@ -502,26 +614,21 @@ int check_astc(const AkvAttnParams* p) {
     return 0;
 }
 
-// Chunk shape: the most block rows whose blocks fit the header stage and whose
-// tokens, rounded up to whole 16-token tiles, fit the LDS tile; never more
-// than one split. The FP16 control uses whole LDS tiles.
-template <int D, int NCH, bool ASTC>
-int plan_chunks(const AkvAttnParams* p, KernelArgs* a) {
-    using C = Cfg<D, NCH, ASTC>;
-    if (!ASTC) {
-        a->chunk_rows = 0;
-        a->chunk_tokens = C::kVtTok;
-    } else {
-        const uint32_t cols = p->atlas_cols, by = p->block_y;
-        uint32_t r = uint32_t(C::kMaxBlocks) / cols;
-        while (r > 0 && (r * by + 15) / 16 * 16 > uint32_t(C::kVtTok)) --r;
+// Chunk shape. ASTC V: the most whole block rows whose blocks fit the header
+// stage and whose tokens fit a chunk; FP16 control: a whole chunk. Never more
+// than one split.
+template <int D, int NCH>
+int plan_chunks(const AkvAttnParams* p, bool astc, KernelArgs* a) {
+    using C = Cfg<D, NCH>;
+    uint32_t tokens = C::kMaxTok;
+    if (astc) {
+        const uint32_t by = p->block_y;
+        uint32_t r = uint32_t(C::kMaxBlocks) / p->atlas_cols;
+        if (r * by > uint32_t(C::kMaxTok)) r = uint32_t(C::kMaxTok) / by;
         if (r == 0) return AKV_HIP_ERR_SHAPE;
-        const uint32_t tile_rows = p->tile_tokens / by;
-        if (tile_rows < r) r = tile_rows;
-        a->chunk_rows = r;
-        a->chunk_tokens = r * by;
+        tokens = r * by;
     }
-    if (a->chunk_tokens > p->tile_tokens) a->chunk_tokens = p->tile_tokens;
+    a->chunk_tokens = tokens < p->tile_tokens ? tokens : p->tile_tokens;
     return 0;
 }
 
@@ -535,9 +642,8 @@ int make_args(const AkvAttnParams* p, bool astc, KernelArgs* a) {
     }
     a->qscale = float(1.4426950408889634 / std::sqrt(double(p->dim)));
     const bool scalar = astc && p->layout == AKV_LAYOUT_SCALAR;
-    if (!astc) return p->dim == 64 ? plan_chunks<64, 4, false>(p, a) : plan_chunks<128, 4, false>(p, a);
-    if (p->dim == 64) return scalar ? plan_chunks<64, 1, true>(p, a) : plan_chunks<64, 4, true>(p, a);
-    return scalar ? plan_chunks<128, 1, true>(p, a) : plan_chunks<128, 4, true>(p, a);
+    if (p->dim == 64) return scalar ? plan_chunks<64, 1>(p, astc, a) : plan_chunks<64, 4>(p, astc, a);
+    return scalar ? plan_chunks<128, 1>(p, astc, a) : plan_chunks<128, 4>(p, astc, a);
 }
 
 struct Ptrs {
@@ -553,15 +659,20 @@ struct Ptrs {
     uint16_t* dump;
 };
 
-template <int D, int NCH, bool ASTC, bool DUMP>
-hipError_t launch_g(const KernelArgs& a, uint32_t G, const Ptrs& x, hipStream_t st) {
+template <int D, int NCH, bool DUMP>
+hipError_t launch_astc_g(const KernelArgs& a, uint32_t G, const Ptrs& x, hipStream_t st) {
     dim3 grid(a.p.splits, a.p.kv_heads, a.p.batch);
     auto* s2 = reinterpret_cast<float2*>(x.stats);
+    if constexpr (DUMP) {
+        astc_attn_kernel<D, NCH, 1, true><<<grid, kThreads, 0, st>>>(a, x.q, x.k, x.vblk, x.vs, x.vo, x.tab, x.partial,
+                                                                      s2, x.dump);
+        return hipGetLastError();
+    }
     switch (G) {
-#define AKV_CASE(GG)                                                                                             \
-    case GG:                                                                                                     \
-        attn_kernel<D, NCH, GG, ASTC, DUMP><<<grid, kThreads, 0, st>>>(a, x.q, x.k, x.vblk, x.vh, x.vs, x.vo,   \
-                                                                        x.tab, x.partial, s2, x.dump);          \
+#define AKV_CASE(GG)                                                                                       \
+    case GG:                                                                                               \
+        astc_attn_kernel<D, NCH, GG, DUMP><<<grid, kThreads, 0, st>>>(a, x.q, x.k, x.vblk, x.vs, x.vo, x.tab, \
+                                                                       x.partial, s2, x.dump);            \
         break;
         AKV_CASE(1)
         AKV_CASE(2)
@@ -575,17 +686,32 @@ hipError_t launch_g(const KernelArgs& a, uint32_t G, const Ptrs& x, hipStream_t 
     return hipGetLastError();
 }
 
-template <bool ASTC, bool DUMP>
-hipError_t launch(const KernelArgs& a, uint32_t G, const Ptrs& x, hipStream_t st) {
-    if constexpr (ASTC) {
-        const bool scalar = a.p.layout == AKV_LAYOUT_SCALAR;
-        if (a.p.dim == 64)
-            return scalar ? launch_g<64, 1, true, DUMP>(a, G, x, st) : launch_g<64, 4, true, DUMP>(a, G, x, st);
-        return scalar ? launch_g<128, 1, true, DUMP>(a, G, x, st) : launch_g<128, 4, true, DUMP>(a, G, x, st);
-    } else {
-        if (a.p.dim == 64) return launch_g<64, 4, false, false>(a, G, x, st);
-        return launch_g<128, 4, false, false>(a, G, x, st);
+template <bool DUMP>
+hipError_t launch_astc(const KernelArgs& a, uint32_t G, const Ptrs& x, hipStream_t st) {
+    const bool scalar = a.p.layout == AKV_LAYOUT_SCALAR;
+    if (a.p.dim == 64) return scalar ? launch_astc_g<64, 1, DUMP>(a, G, x, st) : launch_astc_g<64, 4, DUMP>(a, G, x, st);
+    return scalar ? launch_astc_g<128, 1, DUMP>(a, G, x, st) : launch_astc_g<128, 4, DUMP>(a, G, x, st);
+}
+
+template <int D>
+hipError_t launch_fp16_g(const KernelArgs& a, uint32_t G, const Ptrs& x, hipStream_t st) {
+    dim3 grid(a.p.splits, a.p.kv_heads, a.p.batch);
+    auto* s2 = reinterpret_cast<float2*>(x.stats);
+    switch (G) {
+#define AKV_CASE(GG)                                                                                   \
+    case GG:                                                                                           \
+        fp16_attn_kernel<D, GG><<<grid, kThreads, 0, st>>>(a, x.q, x.k, x.vh, x.partial, s2);         \
+        break;
+        AKV_CASE(1)
+        AKV_CASE(2)
+        AKV_CASE(3)
+        AKV_CASE(4)
+        AKV_CASE(8)
+#undef AKV_CASE
+        default:
+            return hipErrorInvalidValue;
     }
+    return hipGetLastError();
 }
 
 int as_int(hipError_t e) { return e == hipSuccess ? 0 : int(e); }
@@ -611,7 +737,7 @@ int run_astc(const AkvAttnParams* p, const float* q, const uint16_t* k, const vo
     if (int rc = make_args(p, true, &a)) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const Ptrs x{q, k, static_cast<const uint4*>(v_blocks), nullptr, v_scale, v_offset, tab, partial, stats, nullptr};
-    hipError_t e = launch<true, false>(a, G, x, st);
+    hipError_t e = launch_astc<false>(a, G, x, st);
     if (e == hipSuccess && with_merge) e = launch_merge(p, partial, stats, out, st);
     return as_int(e);
 }
@@ -652,7 +778,7 @@ int akv_hip_fp16_attention(const AkvAttnParams* p, const float* q, const uint16_
     if (int rc = make_args(p, false, &a)) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const Ptrs x{q, k, nullptr, v, nullptr, nullptr, nullptr, partial, stats, nullptr};
-    hipError_t e = launch<false, false>(a, G, x, st);
+    hipError_t e = p->dim == 64 ? launch_fp16_g<64>(a, G, x, st) : launch_fp16_g<128>(a, G, x, st);
     if (e == hipSuccess) e = launch_merge(p, partial, stats, out, st);
     return as_int(e);
 }
@@ -668,7 +794,7 @@ int akv_hip_decode_values(const AkvAttnParams* p, const void* v_blocks, uint16_t
     if (int rc = make_args(p, true, &a)) return rc;
     const Ptrs x{nullptr, nullptr, static_cast<const uint4*>(v_blocks), nullptr, nullptr, nullptr, tab, nullptr,
                  nullptr, u};
-    return as_int(launch<true, true>(a, G, x, static_cast<hipStream_t>(stream)));
+    return as_int(launch_astc<true>(a, 1, x, static_cast<hipStream_t>(stream)));
 }
 
 int akv_hip_decode_blocks(const void* blocks, size_t n, unsigned bx, unsigned by, uint16_t* texels, void* stream) {
