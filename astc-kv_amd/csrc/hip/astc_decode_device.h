@@ -552,7 +552,7 @@ __device__ __attribute__((always_inline)) inline void decode_header(const LdsTab
 // Weight field `idx` (grid order, planes interleaved) of a block.
 template <int NCH>
 __device__ inline uint32_t field_at(const BlockDesc<NCH>& d, uint32_t nb, int idx) {
-    const uint32_t pos = uint32_t(idx) * nb, w = pos >> 5;
+    const uint32_t pos = __umul24(uint32_t(idx), nb), w = pos >> 5;
     return __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(d.qw[w + 1], d.qw[w], pos & 31), 0, nb);
 }
 
@@ -609,6 +609,40 @@ __device__ inline uint2 texel_fp16(const BlockDesc<NCH>& d, const LdsTables& L, 
         else return uint2{reinterpret_cast<const uint16_t*>(d.tab)[entry], 0u};
     }
     return texel_compute<NCH>(d, L, f.bx, f.ds, f.dt, x, y, p);
+}
+
+// Stage 2 for K texels at once, the way the attention loop needs them: the
+// table lookups of all K are straight-line code (their LDS reads issue
+// together), and the compute path runs only where a block needs it. The
+// table read of a block that is not a table may land anywhere in the first
+// kilobyte past its record (entry < 128); its value is replaced.
+template <int NCH, int K>
+__device__ inline void texels_fp16(const BlockDesc<NCH>* desc, const int (&blk)[K], const int (&i)[K],
+                                   const int (&x)[K], const int (&y)[K], const LdsTables& L, Footprint f,
+                                   uint2 (&out)[K]) {
+    uint32_t info[K];
+    int p[K];
+    bool all_table = true;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        info[k] = desc[blk[k]].info;
+        p[k] = int(__builtin_amdgcn_ubfe(desc[blk[k]].part[i[k] >> 4], 2 * (i[k] & 15), 2));
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const BlockDesc<NCH>& d = desc[blk[k]];
+        const uint32_t nb = (info[k] >> kInfoNbShift) & 7;
+        const int entry = int(__umul24(uint32_t(p[k]), (info[k] >> kInfoLevelsShift) & 63)) + int(field_at(d, nb, i[k]));
+        if constexpr (NCH == 4) out[k] = *reinterpret_cast<const uint2*>(&d.tab[2 * entry]);
+        else out[k] = uint2{reinterpret_cast<const uint16_t*>(d.tab)[entry], 0u};
+        all_table = all_table && (info[k] & kInfoTable);
+    }
+    if (!all_table) {
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+            if (!(info[k] & kInfoTable))
+                out[k] = texel_compute<NCH>(desc[blk[k]], L, f.bx, f.ds, f.dt, x[k], y[k], p[k]);
+    }
 }
 
 }  // namespace akv_hip

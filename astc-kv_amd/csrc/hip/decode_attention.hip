@@ -71,8 +71,9 @@ struct KernelArgs {
 };
 
 // a / d with magic = ceil(2^24 / d): exact when a * d < 2^24 (the error term
-// a * (magic * d - 2^24) stays below 2^24), which holds for every use below.
-__device__ inline uint32_t fdiv(uint32_t a, uint32_t magic) { return (a * magic) >> 24; }
+// a * (magic * d - 2^24) stays below 2^24), which holds for every use below;
+// a and magic fit 24 bits and a * magic fits 32, so one 24-bit multiply.
+__device__ inline uint32_t fdiv(uint32_t a, uint32_t magic) { return __umul24(a, magic) >> 24; }
 __device__ inline float half_to_float(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
 
 // Channel held by row `row` of MFMA row block `mb` of P.V. RGBA texels (and the
@@ -134,14 +135,16 @@ __device__ inline void attend_tile(const uint4* kr, const half4* qhi, const half
     mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
     const float m_new = fmaxf(m_run, mt);   // finite: token 0 of the tile exists
-    const float alpha = exp2f(m_run - m_new);
+    // v_exp_f32 directly: exact to ~1 ulp for normal results; results below
+    // 2^-126 (weights under 1e-38 of the running maximum) flush to zero.
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
     m_run = m_new;
     const uint32_t sov[4] = {so4.x, so4.y, so4.z, so4.w};
     float psum = 0.0f, poff = 0.0f;
     half4 phi, plo;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float pr = exp2f(s[i] - m_new);
+        const float pr = __builtin_amdgcn_exp2f(s[i] - m_new);
         psum += pr;
         float pv = pr;
         if constexpr (AFFINE) {
@@ -287,8 +290,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
         const int nblk = chunk_blocks(c0);
         // 1. Loads, in the order they are needed.
         const uint4 pw = tid < nblk ? partition_words(raw, tab) : uint4{0, 0, 0, 0};
-        uint4 kcur[C::kRowLoads];
-        if constexpr (!DUMP) load_k_tile<D>(kcur, kseq + size_t(c0) * D, 16 * wave, ntok, lane);
+        uint4 kcur[C::kRowLoads], knext[C::kRowLoads];
+        if constexpr (!DUMP) {
+            load_k_tile<D>(kcur, kseq + size_t(c0) * D, 16 * wave, ntok, lane);
+            load_k_tile<D>(knext, kseq + size_t(c0) * D, 16 * (wave + kWaves), ntok, lane);
+        }
         uint32_t so = 0;
         if (!DUMP && tid < ntok) so = uint32_t(sseq[c0 + tid]) | (uint32_t(oseq[c0 + tid]) << 16);
         const uint4 raw_now = raw;
@@ -322,26 +328,43 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
         __syncthreads();
         if (tid < nblk) decode_header<NCH>(sh.tabs, sh.u.h.desc[sh.order[tid]], sh.u.h.cv[tid]);
         __syncthreads();
-        // 3. This wave's tiles (every fourth): K rows of the next one are
-        // requested first, then texels straight into MFMA operands, then attention.
+        // 3. This wave's tiles (every fourth): the K rows of the tile after
+        // next are requested first, then texels go straight into MFMA
+        // operands, then attention.
 #pragma unroll 1
         for (int t0 = 16 * wave; t0 < ntok; t0 += 16 * kWaves) {
-            uint4 knext[C::kRowLoads];
-            if constexpr (!DUMP) load_k_tile<D>(knext, kseq + size_t(c0) * D, t0 + 16 * kWaves, ntok, lane);
+            uint4 kafter[C::kRowLoads];   // two tiles ahead
+            if constexpr (!DUMP) load_k_tile<D>(kafter, kseq + size_t(c0) * D, t0 + 32 * kWaves, ntok, lane);
             const int tq = t0 + 4 * g;   // this lane's 4 tokens: tq .. tq + 3
-            int r = int(fdiv(uint32_t(tq), a.mag_by)), y = tq - r * by;
+            // Tokens past the chunk decode the chunk's last token; zeroed below.
+            int rk[4], yk[4];
+            {
+                const int tl = min(tq, ntok - 1);
+                int r = int(fdiv(uint32_t(tl), a.mag_by)), y = tl - r * by;
+#pragma unroll
+                for (int tk = 0; tk < 4; ++tk) {
+                    rk[tk] = int(__umul24(uint32_t(r), cols));
+                    yk[tk] = y;
+                    if (tq + tk + 1 < ntok && ++y == by) {
+                        y = 0;
+                        ++r;
+                    }
+                }
+            }
             uint2 tx[4][C::kColGroups];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int kc = 0; kc < C::kColGroups; ++kc) {
+                int bk[4], ik[4], xk[4];
 #pragma unroll
-                for (int kc = 0; kc < C::kColGroups; ++kc)
-                    tx[i][kc] = tq + i < ntok ? texel_fp16<NCH>(sh.u.h.desc[r * int(cols) + bcol[kc]], sh.tabs, f,
-                                                                xin[kc], y)
-                                              : uint2{0, 0};
-                if (++y == by) {
-                    y = 0;
-                    ++r;
+                for (int tk = 0; tk < 4; ++tk) {
+                    bk[tk] = rk[tk] + bcol[kc];
+                    ik[tk] = int(__umul24(uint32_t(yk[tk]), uint32_t(f.bx))) + xin[kc];
+                    xk[tk] = xin[kc];
                 }
+                uint2 tv[4];
+                texels_fp16<NCH, 4>(sh.u.h.desc, bk, ik, xk, yk, sh.tabs, f, tv);
+#pragma unroll
+                for (int tk = 0; tk < 4; ++tk) tx[tk][kc] = tq + tk < ntok ? tv[tk] : uint2{0, 0};
             }
             if constexpr (DUMP) {
                 uint16_t* dst = dump + (seq_kv * p.tokens + c0) * D;
@@ -379,7 +402,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
             const uint4 so4 = *reinterpret_cast<const uint4*>(&sh.so[tq]);
             attend_tile<D, true>(kcur, qhi, qlo, va, so4, ntok - t0, g, m_run, l_run, off_run, o);
 #pragma unroll
-            for (int L = 0; L < C::kRowLoads; ++L) kcur[L] = knext[L];
+            for (int L = 0; L < C::kRowLoads; ++L) {
+                kcur[L] = knext[L];
+                knext[L] = kafter[L];
+            }
         }
         __syncthreads();   // descriptors and so are rewritten by the next chunk
     }
@@ -396,9 +422,44 @@ struct Fp16Shared {
     WaveStats ws;
 };
 
-// Same tiling, V rows loaded straight into the P.V operand (RGBA-style channel
-// order: lane n16 reads channels 4x .. 4x+3 of texel-column-like group
-// x = n16 + 16k, 8 bytes per token, so 16 lanes read one 128-byte row piece).
+// V rows of one 16-token tile straight into the P.V operand layout
+// (RGBA-style channel order: lane n16 reads channels 4x .. 4x+3 of group
+// x = n16 + 16k for tokens t0 + 4 * (lane / 16) + i, 8 bytes per token, so 16
+// lanes read 128 contiguous bytes). Tokens at or past ntok read as zero.
+template <int D>
+__device__ inline void load_v_tile(uint2 (&r)[4][D / 64], const uint16_t* __restrict__ seq, int t0, int ntok,
+                                   int lane) {
+    const int n16 = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int kc = 0; kc < D / 64; ++kc) {
+            const int t = t0 + 4 * g + i;
+            r[i][kc] = t < ntok ? *reinterpret_cast<const uint2*>(seq + size_t(t) * D + 4 * (n16 + 16 * kc))
+                                : uint2{0, 0};
+        }
+}
+
+template <int D>
+__device__ inline void v_operands(const uint2 (&r)[4][D / 64], half4* va) {
+#pragma unroll
+    for (int kc = 0; kc < D / 64; ++kc) {
+        const uint32_t sel[2] = {0x05040100u, 0x07060302u};
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const uint32_t s = sel[jj & 1];
+            const uint32_t lo = jj < 2 ? __builtin_amdgcn_perm(r[1][kc].x, r[0][kc].x, s)
+                                       : __builtin_amdgcn_perm(r[1][kc].y, r[0][kc].y, s);
+            const uint32_t hi = jj < 2 ? __builtin_amdgcn_perm(r[3][kc].x, r[2][kc].x, s)
+                                       : __builtin_amdgcn_perm(r[3][kc].y, r[2][kc].y, s);
+            va[4 * kc + jj] = __builtin_bit_cast(half4, uint2{lo, hi});
+        }
+    }
+}
+
+// FP16-K/V control: each wave streams its 16-token tiles of the split (every
+// fourth tile), with the K and V rows of the next two tiles in flight while
+// it computes the current one.
 template <int D, int G>
 __global__ __launch_bounds__(kThreads) void fp16_attn_kernel(KernelArgs a, const float* __restrict__ q,
                                                              const uint16_t* __restrict__ k,
@@ -412,11 +473,10 @@ __global__ __launch_bounds__(kThreads) void fp16_attn_kernel(KernelArgs a, const
     const int n16 = lane & 15, g = lane >> 4;
     const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
     const int split_begin = split * int(p.tile_tokens);
-    const int split_end = min(split_begin + int(p.tile_tokens), int(p.tokens));
-    const int CT = int(a.chunk_tokens);
+    const int ntok = min(int(p.tile_tokens), int(p.tokens) - split_begin);
     const size_t seq_kv = size_t(b) * p.kv_heads + kh;
-    const uint16_t* kseq = k + seq_kv * p.tokens * D;
-    const uint16_t* vseq = v + seq_kv * p.tokens * D;
+    const uint16_t* kseq = k + (seq_kv * p.tokens + split_begin) * D;
+    const uint16_t* vseq = v + (seq_kv * p.tokens + split_begin) * D;
 
     half4 qhi[C::kKSteps], qlo[C::kKSteps];
     load_q<D, G>(q + (size_t(b) * p.query_heads + size_t(kh) * G) * D, a.qscale, n16, g, qhi, qlo);
@@ -425,45 +485,26 @@ __global__ __launch_bounds__(kThreads) void fp16_attn_kernel(KernelArgs a, const
 #pragma unroll
     for (int mb = 0; mb < C::kMBlocks; ++mb) o[mb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    for (int c0 = split_begin; c0 < split_end; c0 += CT) {
-        const int ntok = min(CT, split_end - c0);
-        uint4 kreg[C::kWaveTiles * C::kRowLoads];
-        uint2 vreg[C::kWaveTiles][4][D / 64];
-#pragma unroll
-        for (int j = 0; j < C::kWaveTiles; ++j) {
-            const int t0 = 16 * (wave + kWaves * j);
-            load_k_tile<D>(kreg + j * C::kRowLoads, kseq + size_t(c0) * D, t0, ntok, lane);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int kc = 0; kc < D / 64; ++kc) {
-                    const int t = t0 + 4 * g + i;
-                    vreg[j][i][kc] = t < ntok ? *reinterpret_cast<const uint2*>(vseq + size_t(c0 + t) * D +
-                                                                                 4 * (n16 + 16 * kc))
-                                              : uint2{0, 0};
-                }
-        }
-#pragma unroll
-        for (int j = 0; j < C::kWaveTiles; ++j) {
-            const int t0 = 16 * (wave + kWaves * j);
-            if (t0 >= ntok) break;
-            half4 va[C::kMBlocks];
-#pragma unroll
-            for (int kc = 0; kc < D / 64; ++kc) {
-                const uint32_t sel[2] = {0x05040100u, 0x07060302u};
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj) {
-                    const uint32_t s = sel[jj & 1];
-                    const uint32_t lo = jj < 2 ? __builtin_amdgcn_perm(vreg[j][1][kc].x, vreg[j][0][kc].x, s)
-                                               : __builtin_amdgcn_perm(vreg[j][1][kc].y, vreg[j][0][kc].y, s);
-                    const uint32_t hi = jj < 2 ? __builtin_amdgcn_perm(vreg[j][3][kc].x, vreg[j][2][kc].x, s)
-                                               : __builtin_amdgcn_perm(vreg[j][3][kc].y, vreg[j][2][kc].y, s);
-                    va[4 * kc + jj] = __builtin_bit_cast(half4, uint2{lo, hi});
-                }
-            }
-            attend_tile<D, false>(kreg + j * C::kRowLoads, qhi, qlo, va, uint4{0, 0, 0, 0}, ntok - t0, g, m_run,
-                                  l_run, off_run, o);
-        }
+    constexpr int kStride = 16 * kWaves;
+    uint4 k0[C::kRowLoads], k1[C::kRowLoads];
+    uint2 v0[4][D / 64], v1[4][D / 64];
+    int t0 = 16 * wave;
+    load_k_tile<D>(k0, kseq, t0, ntok, lane);
+    load_v_tile<D>(v0, vseq, t0, ntok, lane);
+    load_k_tile<D>(k1, kseq, t0 + kStride, ntok, lane);
+    load_v_tile<D>(v1, vseq, t0 + kStride, ntok, lane);
+    half4 va[C::kMBlocks];
+    for (; t0 < ntok; t0 += 2 * kStride) {
+        v_operands<D>(v0, va);
+        attend_tile<D, false>(k0, qhi, qlo, va, uint4{0, 0, 0, 0}, ntok - t0, g, m_run, l_run, off_run, o);
+        load_k_tile<D>(k0, kseq, t0 + 2 * kStride, ntok, lane);
+        load_v_tile<D>(v0, vseq, t0 + 2 * kStride, ntok, lane);
+        if (t0 + kStride >= ntok) break;
+        v_operands<D>(v1, va);
+        attend_tile<D, false>(k1, qhi, qlo, va, uint4{0, 0, 0, 0}, ntok - t0 - kStride, g, m_run, l_run, off_run,
+                              o);
+        load_k_tile<D>(k1, kseq, t0 + 3 * kStride, ntok, lane);
+        load_v_tile<D>(v1, vseq, t0 + 3 * kStride, ntok, lane);
     }
     __syncthreads();
     combine_waves<D, 4, G>(sh.comb, sh.ws, o, m_run, l_run, off_run, partial, stats,
