@@ -209,12 +209,15 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, atlas: DeviceAtlas, tile:
     return (out, partial, stats) if return_states else out
 
 
-def fp16_params(batch, kv_heads, query_heads, tokens, dim, tile=None) -> AkvAttnParams:
+def fp16_params(batch, kv_heads, query_heads, tokens, dim, tile=None, cu_count: int = 256) -> AkvAttnParams:
+    """The FP16 control streams 16-token tiles per wave, so its default split is
+    about one round of 3 resident workgroups per CU (at least 64 tokens)."""
     def build(t):
         return AkvAttnParams(batch, tokens, query_heads, kv_heads, dim, 0, t, -(-tokens // t), 0, 0, 0, 0, 0)
 
     if tile is None:
-        tile = default_tile(batch, kv_heads, tokens, task_tokens(build(tokens), astc=False))
+        splits = max(1, -(-3 * cu_count // (batch * kv_heads)))
+        tile = max(64, -(-(-(-tokens // splits)) // 16) * 16)
     return build(tile)
 
 

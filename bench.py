@@ -13,10 +13,21 @@ from a HIP graph, with events on the launch stream.
 
 Prints one JSON line. `value` is the effective bandwidth: algorithmic bytes
 of a step (K + ASTC blocks read + V scale/offset + q + out) / step time.
+`roofline.achieved` is the split kernel's algorithmic bytes (K + ASTC blocks
++ V scale/offset + q) / its own launch time. `roofline.traffic` is the HBM
+traffic per split launch that rocprofv3 measured (FETCH_SIZE + WRITE_SIZE,
+scaled by a plain copy kernel of known size) for this same workload, read from
+the committed profile summary when its workload line matches.
+
+`python bench.py --summarize KT FETCH WRITE` instead prints a markdown summary
+of rocprofv3 CSV output directories (kernel trace with --stats, a FETCH_SIZE
+pass, a WRITE_SIZE pass) of a bench run made with --copy-calibration-mb.
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
 import sys
@@ -31,10 +42,16 @@ for _p in (ROOT, ROOT / "astc-kv_amd"):
         sys.path.insert(0, str(_p))
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "astc_split_kernel_T8192_b16_rgba6x5.md"
+COPY_KERNEL = "neg_kernel"   # the calibration copy: torch.neg over float32 (reads N bytes, writes N bytes)
+
+
+def log(msg: str):
+    print(f"# {msg}", file=sys.stderr, flush=True)
 
 
 def parse_args(argv=None):
-    ap = argparse.ArgumentParser(description=__doc__)
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
@@ -47,13 +64,25 @@ def parse_args(argv=None):
     ap.add_argument("--block", default="6x5")
     ap.add_argument("--page", type=int, default=120)
     ap.add_argument("--tile", type=int, default=0, help="tokens per split (0 = automatic)")
+    ap.add_argument("--fp16-tile", type=int, default=0, help="tokens per split of the FP16 control (0 = automatic)")
     ap.add_argument("--quality", type=float, default=50.0, help="encoder effort for the synthetic V atlas")
     ap.add_argument("--pool-mb", type=float, default=600.0, help="minimum bytes of distinct KV sets rotated")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--copy-calibration-mb", type=float, default=0.0,
+                    help="also run a plain copy kernel over this many MB (for rocprofv3 counter scaling)")
+    ap.add_argument("--traffic", default=str(TRAFFIC_FILE), help="profile summary holding the measured traffic")
+    ap.add_argument("--summarize", nargs=3, metavar=("KT", "FETCH", "WRITE"),
+                    help="print a markdown summary of rocprofv3 CSV output directories and exit")
     ap.add_argument("--out", default="", help="also write the JSON line to this file")
     return ap.parse_args(argv)
+
+
+def workload_name(a) -> str:
+    bx, by = a.block.split("x")
+    return (f"decode attention T{a.tokens} batch {a.batch}, {a.query_heads}q/{a.kv_heads}kv, D{a.dim}, "
+            f"FP16 K + ASTC {a.layout.upper()} {bx}x{by} V (page {a.page})")
 
 
 def make_inputs(a, rng_seed=20261201):
@@ -72,7 +101,7 @@ def make_inputs(a, rng_seed=20261201):
 
 
 def step_bytes(a, atlas):
-    """Algorithmic bytes of one decode step and of one split launch."""
+    """Algorithmic bytes of one decode step; `split` = what the split kernel must read."""
     b, hq, hkv, t, d = a.batch, a.query_heads, a.kv_heads, a.tokens, a.dim
     rows_read = -(-t // atlas.block_y)
     k_bytes = b * hkv * t * d * 2
@@ -81,6 +110,7 @@ def step_bytes(a, atlas):
     q_bytes = b * hq * d * 4
     out_bytes = b * hq * d * 4
     return {"k": k_bytes, "v_blocks": v_bytes, "v_meta": meta, "q": q_bytes, "out": out_bytes,
+            "split": k_bytes + v_bytes + meta + q_bytes,
             "step": k_bytes + v_bytes + meta + q_bytes + out_bytes}
 
 
@@ -107,7 +137,7 @@ def time_graph(torch, fn, steps, warmup, use_graph=True):
             torch.cuda.synchronize()
             mode = "hipgraph"
         except Exception as e:  # noqa: BLE001
-            print(f"# graph capture failed ({e}); timing eager launches", file=sys.stderr)
+            log(f"graph capture failed ({e}); timing eager launches")
             graph = None
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -127,6 +157,7 @@ def cpu_baseline(q, k, v_restored, seconds):
     batch (V already decoded, as in the reference's CPU path). Returns
     (median seconds per step with all cores, cores, median with 1 core, reps)."""
     from threadpoolctl import threadpool_limits
+
     from oracle import attention_ref as R
     kf = k.astype(np.float32)
     cores = len(os.sched_getaffinity(0))
@@ -145,8 +176,77 @@ def cpu_baseline(q, k, v_restored, seconds):
     return res[cores][0], cores, res[1][0], res[cores][1]
 
 
+def read_traffic(path: str, workload: str):
+    """Traffic per split launch from a profile summary whose `workload:` line matches."""
+    p = Path(path)
+    if not p.exists():
+        return None
+    fields = {}
+    for line in p.read_text().splitlines():
+        line = line.strip().lstrip("-* ").strip()
+        if ":" in line:
+            key, val = line.split(":", 1)
+            fields[key.strip().strip("`")] = val.strip().strip("`")
+    if fields.get("workload") != workload or "traffic_bytes_per_launch" not in fields:
+        return None
+    return {"bytes": int(fields["traffic_bytes_per_launch"]), "source": str(p.relative_to(ROOT))
+            if p.is_relative_to(ROOT) else str(p)}
+
+
+# --- rocprofv3 summary ----------------------------------------------------------------
+
+def _short(name: str) -> str:
+    name = name.replace("akv_hip::", "").replace("void ", "")
+    return name[: name.index("(")] if "(" in name else name
+
+
+def _counter_means(directory: str, counter: str):
+    sums, counts = {}, {}
+    for f in glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] != counter:
+                continue
+            k = _short(r["Kernel_Name"])
+            sums[k] = sums.get(k, 0.0) + float(r["Counter_Value"])
+            counts[k] = counts.get(k, 0) + 1
+    return {k: sums[k] / counts[k] for k in sums}
+
+
+def summarize(kt_dir: str, fetch_dir: str, write_dir: str, calib_mb: float, workload: str) -> str:
+    rows = []
+    for f in glob.glob(os.path.join(kt_dir, "**", "*kernel_stats.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            rows.append((_short(r["Name"]), int(r["Calls"]), float(r["AverageNs"]) / 1e3, float(r["MinNs"]) / 1e3,
+                         float(r["MaxNs"]) / 1e3))
+    fetch = _counter_means(fetch_dir, "FETCH_SIZE")
+    write = _counter_means(write_dir, "WRITE_SIZE")
+    out = ["| kernel | calls | avg µs | min µs | max µs | FETCH_SIZE KiB/dispatch | WRITE_SIZE KiB/dispatch |",
+           "|---|---|---|---|---|---|---|"]
+    for name, calls, avg, mn, mx in sorted(rows, key=lambda r: -r[1] * r[2]):
+        out.append(f"| `{name}` | {calls} | {avg:.2f} | {mn:.2f} | {mx:.2f} | "
+                   f"{fetch.get(name, float('nan')):.1f} | {write.get(name, float('nan')):.1f} |")
+    text = "\n".join(out) + "\n"
+    copy = [k for k in fetch if COPY_KERNEL in k]
+    split = [k for k in fetch if k.startswith("astc_attn_kernel") and ", false>" in k]
+    if copy and calib_mb > 0:
+        nbytes = calib_mb * 1e6
+        ff = nbytes / (fetch[copy[0]] * 1024)
+        wf = nbytes / (write.get(copy[0], float("nan")) * 1024)
+        text += (f"\ncopy calibration (`{copy[0]}`, {calib_mb:g} MB read + {calib_mb:g} MB written): "
+                 f"bytes per FETCH_SIZE byte = {ff:.4f}, bytes per WRITE_SIZE byte = {wf:.4f}\n")
+        if split:
+            fb = fetch[split[0]] * 1024 * ff
+            wb = write.get(split[0], 0.0) * 1024 * wf
+            text += (f"\n- workload: {workload}\n- kernel: `{split[0]}`\n- fetch_bytes_per_launch: {fb:.0f}\n"
+                     f"- write_bytes_per_launch: {wb:.0f}\n- traffic_bytes_per_launch: {fb + wb:.0f}\n")
+    return text
+
+
 def main(argv=None):
     a = parse_args(argv)
+    if a.summarize:
+        print(summarize(*a.summarize, a.copy_calibration_mb, workload_name(a)))
+        return 0
     if a.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported (run with --gpus 1)",
               file=sys.stderr)
@@ -154,11 +254,12 @@ def main(argv=None):
     import torch
 
     from astc_kv import gpu
-    from astc_kv.atlas import build_atlas
+    from astc_kv.atlas import Atlas, build_atlas
     from oracle import astc_oracle as O
     from oracle import attention_ref as R
 
     bx, by = (int(x) for x in a.block.split("x"))
+    log(f"encoding the V atlas: {workload_name(a)}")
     t_setup = time.perf_counter()
     q, k, v = make_inputs(a)
     atlas = build_atlas(v, a.layout, (bx, by), a.page, a.quality)
@@ -166,8 +267,7 @@ def main(argv=None):
     dev = gpu.DeviceAtlas.from_host(atlas)
     qt = torch.from_numpy(q).cuda()
     kt = torch.from_numpy(k).cuda()
-    tile = a.tile or None
-    params = gpu.make_params(dev, a.query_heads, tile)
+    params = gpu.make_params(dev, a.query_heads, a.tile or None)
     nbytes = step_bytes(a, atlas)
     set_bytes = kt.numel() * 2 + dev.nbytes() + qt.numel() * 4
     pool_n = max(1, int(np.ceil(a.pool_mb * 1e6 / set_bytes)))
@@ -176,6 +276,15 @@ def main(argv=None):
     partial = torch.empty((a.batch, a.query_heads, s, a.dim), dtype=torch.float32, device="cuda")
     stats = torch.empty((a.batch, a.query_heads, s, 2), dtype=torch.float32, device="cuda")
     out = torch.empty((a.batch, a.query_heads, a.dim), dtype=torch.float32, device="cuda")
+
+    if a.copy_calibration_mb > 0:
+        n = int(a.copy_calibration_mb * 1e6) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
 
     def step(i):
         kk, dd = pool[i % pool_n]
@@ -187,6 +296,7 @@ def main(argv=None):
         gpu.attention_split(qt, kk, dd, params, partial, stats)
 
     torch.cuda.synchronize()
+    log(f"timing {a.steps} steps (tile {params.tile_tokens}, {s} splits, pool of {pool_n} KV sets)")
     ms_step, mode = time_graph(torch, step, a.steps, a.warmup, not a.no_graph)
     ms_split, _ = time_graph(torch, split_only, a.steps, a.warmup, not a.no_graph)
 
@@ -197,10 +307,11 @@ def main(argv=None):
     ms_resident, _ = time_graph(torch, resident, a.steps, a.warmup, not a.no_graph)
 
     # FP16 K/V control on the same workload (V = restored values rounded to fp16).
+    log("timing the FP16-K/V control")
     u = gpu.decode_values(dev)
     v16 = (u.float() * dev.scale.float()[..., None] + dev.offset.float()[..., None]).half()
     del u
-    fparams = gpu.fp16_params(a.batch, a.kv_heads, a.query_heads, a.tokens, a.dim)
+    fparams = gpu.fp16_params(a.batch, a.kv_heads, a.query_heads, a.tokens, a.dim, a.fp16_tile or None)
     fpool = [(kt, v16)] + [(kt.clone(), v16.clone()) for _ in range(max(1, int(np.ceil(
         a.pool_mb * 1e6 / (kt.numel() * 4)))) - 1)]
     fpart = torch.empty((a.batch, a.query_heads, fparams.splits, a.dim), dtype=torch.float32, device="cuda")
@@ -212,13 +323,14 @@ def main(argv=None):
 
     ms_fp16, _ = time_graph(torch, fstep, a.steps, a.warmup, not a.no_graph)
     fp16_bytes = nbytes["k"] * 2 + nbytes["q"] + nbytes["out"]
+    del fpool
 
     # Correctness of the measured configuration on two sequences (oracle decode + NumPy attention).
+    log("checking two sequences against the oracle")
     step(0)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     sub = [0, a.batch - 1]
-    from astc_kv.atlas import Atlas
     small = Atlas(atlas.blocks[sub], atlas.scale[sub], atlas.offset[sub], a.tokens, a.dim, a.layout, bx, by, a.page)
     tex, _ = O.decode_blocks_fp16(small.blocks.reshape(-1, 16), bx, by)
     bb, hh, rr, cc = small.blocks.shape[:4]
@@ -232,7 +344,10 @@ def main(argv=None):
 
     cpu = None
     if not a.no_cpu:
+        log("timing the CPU baseline (oracle decode + NumPy attention)")
+        t0 = time.perf_counter()
         tex_all, _ = O.decode_blocks_fp16(atlas.blocks.reshape(-1, 16), bx, by)
+        decode_s = time.perf_counter() - t0
         bb, hh, rr, cc = atlas.blocks.shape[:4]
         img = tex_all.reshape(bb, hh, rr, cc, by, bx, 4).transpose(0, 1, 2, 4, 3, 5, 6)
         img = img.reshape(bb, hh, rr * by, cc * bx, 4)[:, :, : a.tokens].astype(np.float32)
@@ -242,15 +357,17 @@ def main(argv=None):
                                  atlas.offset.astype(np.float32)[..., None])
         del tex_all, img, un
         sec, cores, sec1, reps = cpu_baseline(q, k, v_rest, a.cpu_seconds)
-        cpu = {"value": nbytes["step"] / sec / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
-               "sample": f"full workload (batch {a.batch}, T{a.tokens}), median of {reps} steps of the oracle's "
-                         f"NumPy attention (astc_kv/codec.py:253-267) on pre-decoded V; {sec*1e6:.0f} us/step "
-                         f"on {cores} cores, {sec1*1e6:.0f} us/step on 1 core",
-               "us_per_step": sec * 1e6, "us_per_step_1core": sec1 * 1e6}
+        cpu = {"value": round(nbytes["step"] / sec / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+               "sample": f"full workload (batch {a.batch}, T{a.tokens}): median of {reps} steps of the oracle's "
+                         f"NumPy attention (astc_kv/codec.py:253-267) on pre-decoded V, {sec*1e6:.0f} us/step on "
+                         f"{cores} cores ({sec1*1e6:.0f} us/step on 1 core); the oracle's single-threaded C ASTC "
+                         f"decode of the whole atlas took {decode_s*1e6:.0f} us more, not folded in",
+               "us_per_step": round(sec * 1e6, 1), "us_per_step_1core": round(sec1 * 1e6, 1),
+               "astc_decode_us_1core": round(decode_s * 1e6, 1)}
 
-    split_bytes = nbytes["step"] - nbytes["out"] + partial.numel() * 4 + stats.numel() * 4
-    achieved = split_bytes / (ms_split * 1e-3) / 1e9
+    achieved = nbytes["split"] / (ms_split * 1e-3) / 1e9
     value = nbytes["step"] / (ms_step * 1e-3) / 1e9
+    traffic = read_traffic(a.traffic, workload_name(a))
     line = {
         "metric": "µs per decode-attention step + effective KV GB/s (% HBM peak) at T8192",
         "value": round(value, 2),
@@ -264,23 +381,24 @@ def main(argv=None):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16 K / ASTC V, fp32 accumulate",
+        "dtype": "fp16 K / ASTC V (u16 texels), fp32 accumulate",
         "data": "synthetic (seeded Gaussian K/V/q), V encoded by this package's ASTC encoder",
-        "config": {"workload": f"decode attention T{a.tokens} batch {a.batch}, {a.query_heads}q/{a.kv_heads}kv, "
-                               f"D{a.dim}, FP16 K + ASTC {a.layout.upper()} {bx}x{by} V (page {a.page})",
+        "config": {"workload": workload_name(a),
                    "batch": a.batch, "tokens": a.tokens, "query_heads": a.query_heads, "kv_heads": a.kv_heads,
                    "dim": a.dim, "layout": a.layout, "block": [bx, by], "tile_tokens": params.tile_tokens,
                    "splits": params.splits, "pool_sets": pool_n, "timing": mode,
                    "bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "split_kernel (ASTC V)", "bytes_per_launch": split_bytes,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic["bytes"] if traffic else None,
+                     "traffic_source": traffic["source"] if traffic else None,
+                     "kernel": "astc_attn_kernel (split, ASTC V)", "bytes_per_launch": nbytes["split"],
                      "us_per_launch": round(ms_split * 1e3, 3)},
         "cpu_baseline": cpu,
         "resident_single_set": {"us_per_step": round(ms_resident * 1e3, 3),
                                 "GB/s": round(nbytes["step"] / (ms_resident * 1e-3) / 1e9, 2)},
         "fp16_control": {"us_per_step": round(ms_fp16 * 1e3, 3), "bytes_per_step": fp16_bytes,
-                         "GB/s": round(fp16_bytes / (ms_fp16 * 1e-3) / 1e9, 2),
+                         "GB/s": round(fp16_bytes / (ms_fp16 * 1e-3) / 1e9, 2), "tile_tokens": fparams.tile_tokens,
                          "astc_speedup": round(ms_fp16 / ms_step, 4)},
         "parity": {"sequences_checked": sub, "max_abs_err": max_err, "within_rtol1e-3_atol2e-3": parity},
         "setup_s": round(setup_s, 2),

@@ -1,0 +1,115 @@
+"""The two C-ABI libraries load and export every function their headers
+declare, and the GPU library's host-side validation (no GPU work) rejects bad
+parameters with the documented codes. CPU only."""
+import ctypes as ct
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+PKG = ROOT / "astc-kv_amd" / "astc_kv"
+LIBS = {"astc_kv.h": PKG / "libakv_astc.so", "astc_kv_hip.h": PKG / "libastckv_hip.so"}
+
+
+def declared_functions(header: Path):
+    text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(akv_\w+)\s*\(", text)))
+
+
+@pytest.mark.parametrize("header", sorted(LIBS))
+def test_library_exports_every_declared_function(header):
+    lib_path = LIBS[header]
+    assert lib_path.exists(), f"{lib_path} missing: run astc-kv_amd/build.py"
+    names = declared_functions(ROOT / "include" / header)
+    assert len(names) >= 5
+    lib = ct.CDLL(str(lib_path))
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"{lib_path.name} lacks {missing}"
+
+
+class Params(ct.Structure):
+    _fields_ = [(name, ct.c_uint32) for name in (
+        "batch", "tokens", "query_heads", "kv_heads", "dim", "page_tokens", "tile_tokens", "splits",
+        "layout", "block_x", "block_y", "atlas_rows", "atlas_cols")]
+
+
+@pytest.fixture(scope="module")
+def hip():
+    lib = ct.CDLL(str(LIBS["astc_kv_hip.h"]))
+    lib.akv_hip_task_tokens.argtypes = [ct.POINTER(Params), ct.c_int]
+    lib.akv_hip_task_tokens.restype = ct.c_int
+    lib.akv_hip_error_string.argtypes = [ct.c_int]
+    lib.akv_hip_error_string.restype = ct.c_char_p
+    return lib
+
+
+def c3(**kw):
+    """T8192 batch 16, 9q/3kv, D64, RGBA 6x5 atlas padded to pages of 120 tokens."""
+    p = dict(batch=16, tokens=8192, query_heads=9, kv_heads=3, dim=64, page_tokens=120, tile_tokens=240,
+             splits=35, layout=1, block_x=6, block_y=5, atlas_rows=1656, atlas_cols=3)
+    p.update(kw)
+    return Params(**p)
+
+
+def test_chunk_tokens_follow_the_footprint(hip):
+    # 6x5 RGBA D64: 3 block columns, at most 144 blocks -> 48 block rows = 240 tokens.
+    assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=8190, splits=2)), 1) == 240
+    # A split shorter than a chunk is one chunk.
+    assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=35, splits=235)), 1) == 35
+    # 4x4 RGBA D64: 4 block columns -> 36 block rows = 144 tokens.
+    p = c3(block_x=4, block_y=4, atlas_cols=4, atlas_rows=2048, tile_tokens=8192, splits=1)
+    assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 144
+    # Scalar 6x6 D64: 11 block columns -> 13 rows = 78 tokens.
+    p = c3(layout=0, block_x=6, block_y=6, atlas_cols=11, atlas_rows=1366, tile_tokens=8196, splits=1)
+    assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 78
+    # D128 RGBA 4x4: 8 block columns -> 18 rows = 72 tokens.
+    p = c3(dim=128, block_x=4, block_y=4, atlas_cols=8, atlas_rows=2048, tile_tokens=8192, splits=1)
+    assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 72
+    # FP16 control: whole 256-token chunks (128 for D128).
+    assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=8192, splits=1)), 0) == 256
+    assert hip.akv_hip_task_tokens(ct.byref(c3(dim=128, tile_tokens=8192, splits=1)), 0) == 128
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(dim=96), -2),                               # head dim not 64/128
+    (dict(query_heads=10), -2),                       # Hq not a multiple of Hkv
+    (dict(query_heads=15, kv_heads=3), -2),           # G = 5 unsupported
+    (dict(batch=0), -2),
+    (dict(atlas_cols=4), -2),                         # atlas width inconsistent with dim/layout/footprint
+    (dict(atlas_rows=1000), -2),                      # atlas shorter than the sequence
+    (dict(layout=7), -2),
+    (dict(block_x=3), -3),                            # footprint below 4
+    (dict(block_x=10, block_y=8, atlas_cols=2), -3),  # more than 64 texels
+    (dict(tile_tokens=238, splits=35), -4),           # tile not a multiple of block_y
+    (dict(splits=34), -4),                            # splits != ceil(T / tile)
+    (dict(tile_tokens=0), -4),
+])
+def test_rejected_parameters(hip, kw, code):
+    assert hip.akv_hip_task_tokens(ct.byref(c3(**kw)), 1) == code
+    assert hip.akv_hip_error_string(code).decode() != "unknown error"
+
+
+def test_null_params_and_error_strings(hip):
+    assert hip.akv_hip_task_tokens(None, 1) == -1
+    assert hip.akv_hip_error_string(0) == b"success"
+    assert b"NULL" in hip.akv_hip_error_string(-1)
+    assert hip.akv_hip_error_string(-99) == b"unknown error"
+
+
+def test_bridge_error_strings_and_context():
+    lib = ct.CDLL(str(LIBS["astc_kv.h"]))
+    lib.akv_create.argtypes = [ct.c_uint, ct.c_uint, ct.c_float, ct.c_int, ct.POINTER(ct.c_int)]
+    lib.akv_create.restype = ct.c_void_p
+    lib.akv_destroy.argtypes = [ct.c_void_p]
+    lib.akv_error.argtypes = [ct.c_int]
+    lib.akv_error.restype = ct.c_char_p
+    err = ct.c_int(-1)
+    ctx = lib.akv_create(6, 5, 50.0, 0, ct.byref(err))
+    assert ctx and err.value == 0
+    lib.akv_destroy(ctx)
+    err = ct.c_int(0)
+    assert not lib.akv_create(3, 3, 50.0, 0, ct.byref(err)) and err.value != 0
+    assert lib.akv_error(err.value)
+    err = ct.c_int(0)
+    assert not lib.akv_create(6, 6, 50.0, 1, ct.byref(err)) and err.value != 0   # HDR profile: LDR-only codec

@@ -1,0 +1,233 @@
+"""CPU tests of the drop-in Python API (astc_kv.codec), the product CPU codec
+(libakv_astc.so) against the oracle, and the atlas / host planning helpers.
+
+The first group restates the reference's own numeric tests
+(tests/test_numeric.py:17-74) against this package's codec.py: the transforms
+with the lossy codec replaced by an identity round trip, payload and metadata
+byte accounting, the incomplete-page rule, fp16 metadata bounds, GQA attention
+against a scalar FP64 loop, a constant image through the real codec, and the
+quantiser's byte counts."""
+import ctypes as ct
+from unittest.mock import patch
+
+import numpy as np
+import pytest
+
+from astc_kv import codec
+from astc_kv.atlas import Atlas, build_atlas, texel_columns
+from oracle import astc_oracle as O
+from oracle import attention_ref as R
+
+
+class IdentityAstc:
+    """Stand-in for AstcEncoder whose round trip is lossless (square blocks)."""
+
+    def __init__(self, block, *args):
+        self.block = block
+
+    def close(self):
+        pass
+
+    def roundtrip(self, im):
+        h, w, _ = im.shape
+        b = self.block[0] if isinstance(self.block, tuple) else self.block
+        return bytes(-(-h // b) * -(-w // b) * 16), im.copy(), 0.0
+
+
+def test_transforms_and_permutation_inverses():
+    x = np.random.default_rng(42).normal(size=(3, 288, 64)).astype("f4")
+    configs = [{"layout": "scalar", "block": b, "normalization": "page_channel"} for b in (4, 6, 8)]
+    configs += [{"layout": "rgba", "block": 4, "normalization": "page_channel"},
+                {"layout": "scalar", "block": 6, "normalization": "token"},
+                {"layout": "scalar", "block": 6, "normalization": "block_min", "profile": "hdr"}]
+    configs += [dict(layout="scalar", block=6, normalization="page_channel", permutation=p)
+                for p in ("tokens_within_page", "channels")]
+    with patch("astc_kv.codec.AstcEncoder", IdentityAstc):
+        for cfg in configs:
+            y = codec.encode_tensor(x, cfg)
+            np.testing.assert_allclose(y.decoded, x, rtol=2e-6, atol=2e-6, err_msg=str(cfg))
+
+
+def test_payload_and_metadata_padding():
+    with patch("astc_kv.codec.AstcEncoder", IdentityAstc):
+        x = np.zeros((3, 288, 64), np.float32)
+        p = codec.encode_tensor(x, dict(layout="scalar", block=6, normalization="page_channel"))
+        assert p.width == 66
+        assert p.byte_counts["astc_blocks_including_edge_padding"] == 3 * 48 * 11 * 16
+        assert p.logical_bytes == 3 * 288 * 64 * 4 // 8
+        assert len(p.astc_file(0)) == 16 + 48 * 11 * 16
+        t = codec.encode_tensor(x, dict(layout="scalar", block=6, normalization="token"))
+        assert t.bits_per_scalar == pytest.approx(4 + 1 / 6)
+
+
+def test_no_future_in_incomplete_page():
+    with pytest.raises(ValueError):
+        codec.encode_tensor(np.zeros((1, 97, 64), "f4"), dict(layout="scalar", block=6, normalization="token"))
+
+
+def test_metadata_bounds():
+    x = np.concatenate([np.linspace(-500, 500, 10001), [0, 2 ** -27, -2 ** -27, 1.0004]]).astype("f4")
+    assert np.all(codec.fp16_floor(x).astype("f4") <= x)
+    assert np.all(codec.fp16_ceil(x).astype("f4") >= x)
+    # Tightness: no float16 lies strictly between the bound and x.
+    lo = codec.fp16_floor(x)
+    assert np.all(np.nextafter(lo, np.float16(np.inf)).astype("f4") > x)
+
+
+def test_gqa_causal_against_scalar_oracle():
+    rng = np.random.default_rng(17)
+    q = rng.normal(size=(6, 2, 8)).astype("f4")
+    k = rng.normal(size=(2, 7, 8)).astype("f4")
+    v = rng.normal(size=k.shape).astype("f4")
+    positions = np.array([3, 6])
+    got, p = codec.attention(q, k, v, positions)
+    ref = np.zeros_like(got)
+    for h in range(6):
+        for i, t in enumerate(positions):
+            scores = k[h // 3, : t + 1].astype("f8") @ q[h, i].astype("f8") / np.sqrt(8)
+            w = np.exp(scores - scores.max())
+            w /= w.sum()
+            ref[h, i] = w @ v[h // 3, : t + 1]
+    np.testing.assert_allclose(got, ref, rtol=2e-6, atol=2e-6)
+    assert np.all(p[:, 0, 4:] == 0)
+
+
+@pytest.mark.parametrize("normalization", ["page_channel", "token"])
+def test_real_astc_constants(normalization):
+    x = np.full((1, 96, 64), 3.75, np.float32)
+    y = codec.encode_tensor(x, dict(layout="scalar", block=6, normalization=normalization), quality=10)
+    np.testing.assert_allclose(y.decoded, x, atol=1e-5)
+
+
+def test_hdr_profile_is_rejected_by_the_ldr_codec():
+    x = np.full((1, 96, 64), 3.75, np.float32)
+    with pytest.raises(RuntimeError):
+        codec.encode_tensor(x, dict(layout="scalar", block=6, normalization="block_min", profile="hdr"),
+                            quality=10)
+
+
+def test_quantizer_counts():
+    x = np.random.default_rng(4).normal(size=(3, 288, 64)).astype("f4")
+    for bits in (2, 4, 8):
+        decoded, counts = codec.affine_quantize(x, bits)
+        assert sum(counts.values()) * 8 / x.size == bits + 0.5
+        assert np.isfinite(decoded).all()
+
+
+@pytest.mark.parametrize("bits,axis,group", [(4, "token", 32), (2, "token", 64), (8, "channel", 96)])
+def test_quantizer_codes_match_oracle_and_invariants(bits, axis, group):
+    x = np.random.default_rng(bits).standard_t(3, size=(2, 192, 128)).astype("f4")
+    dec, counts, codes, packed, offset, scale = codec.affine_quantize_codes(x, bits, axis, group)
+    ref = R.affine_quantize(x, bits, axis, group)
+    rdec, rcodes = ref[0], ref[2]
+    np.testing.assert_array_equal(codes.ravel(), rcodes.ravel())
+    np.testing.assert_array_equal(dec, rdec)
+    assert codes.max() <= (1 << bits) - 1
+    # Reconstruction error within half a step of the group's scale.
+    step = np.broadcast_to(scale.astype(np.float32), codes.shape).reshape(x.shape)
+    assert np.all(np.abs(dec - x) <= step / 2 * (1 + 1e-6))
+    # Packing: code i of each run of 8/bits sits at bit (i mod 8/bits) * bits.
+    per = 8 // bits
+    flat = codes.ravel()
+    unpacked = ((packed[:, None] >> (np.arange(per, dtype=np.uint8) * bits)) & ((1 << bits) - 1)).ravel()
+    np.testing.assert_array_equal(unpacked[: flat.size], flat)
+
+
+# --- the product CPU codec against the oracle ------------------------------------
+
+def product_decode(blocks, bx, by):
+    lib = codec.load_codec_library()
+    blocks = np.ascontiguousarray(blocks, np.uint8).reshape(-1, 16)
+    out = np.empty((len(blocks), by, bx, 4), np.uint16)
+    kinds = np.empty(len(blocks), np.int32)
+    rc = lib.akv_decode_blocks_fp16(bx, by, blocks.ctypes.data, len(blocks), out.ctypes.data, kinds.ctypes.data)
+    assert rc == 0
+    return out, kinds
+
+
+def test_product_decoder_matches_oracle_on_reference_fixture(golden):
+    raw = (golden / "t384" / "v-h000.astc").read_bytes()
+    hdr = O.read_astc_file(raw)
+    blocks = np.frombuffer(hdr["payload"], np.uint8).reshape(-1, 16)
+    got, kinds = product_decode(blocks, hdr["bx"], hdr["by"])
+    ref, rkinds = O.decode_blocks_fp16(blocks, hdr["bx"], hdr["by"])
+    np.testing.assert_array_equal(got, ref.view(np.uint16))
+    np.testing.assert_array_equal(kinds, rkinds)
+
+
+@pytest.mark.parametrize("bx,by", [(4, 4), (5, 4), (6, 5), (6, 6), (8, 5), (8, 8)])
+def test_product_decoder_matches_oracle_on_random_blocks(bx, by):
+    blocks = np.random.default_rng(bx * 16 + by).integers(0, 256, size=(20000, 16), dtype=np.uint8)
+    got, kinds = product_decode(blocks, bx, by)
+    ref, rkinds = O.decode_blocks_fp16(blocks, bx, by)
+    np.testing.assert_array_equal(got, ref.view(np.uint16))
+    np.testing.assert_array_equal(kinds, rkinds)
+
+
+@pytest.mark.parametrize("bx,by,quality", [(4, 4, 50), (6, 5, 10), (6, 5, 50), (6, 5, 98), (6, 6, 70), (8, 8, 50)])
+def test_encoder_round_trip(bx, by, quality):
+    """Own encoder output decodes identically in the oracle and the product
+    decoder, and reconstructs smooth and noisy tiles within a loose bound."""
+    rng = np.random.default_rng(quality)
+    n = 256
+    yy, xx = np.meshgrid(np.linspace(0, 1, by), np.linspace(0, 1, bx), indexing="ij")
+    smooth = (0.2 + 0.3 * yy[None, ..., None] + 0.4 * xx[None, ..., None] * rng.random((n, 1, 1, 4)))
+    noisy = np.clip(rng.normal(0.5, 0.15, size=(n, by, bx, 4)), 0, 1)
+    texels = np.concatenate([smooth, noisy]).astype(np.float32)
+    enc = codec.AstcEncoder((bx, by), quality)
+    try:
+        blocks = enc.encode_blocks(texels)
+    finally:
+        enc.close()
+    got, _ = product_decode(blocks, bx, by)
+    ref, kinds = O.decode_blocks_fp16(blocks, bx, by)
+    np.testing.assert_array_equal(got, ref.view(np.uint16))
+    assert np.all(kinds != 2), "encoder emitted an error block"
+    dec = ref.astype(np.float32)
+    assert np.abs(dec[:n] - texels[:n]).mean() < 0.08
+    assert np.sqrt(((dec[n:] - texels[n:]) ** 2).mean()) < 0.15
+
+
+# --- atlas and host planning --------------------------------------------------------
+
+@pytest.mark.parametrize("layout,block,d", [("rgba", (6, 5), 64), ("rgba", (4, 4), 128), ("scalar", (6, 6), 64)])
+def test_atlas_layout_and_restore(layout, block, d):
+    v = np.random.default_rng(3).normal(0, 0.5, size=(2, 2, 250, d)).astype(np.float32)
+    page = {(6, 5): 120, (4, 4): 128, (6, 6): 96}[block]
+    at = build_atlas(v, layout, block, page, quality=50)
+    bx, by = block
+    t_pad = -(-250 // page) * page
+    assert at.blocks.shape == (2, 2, t_pad // by, -(-texel_columns(d, layout) // bx), 16)
+    assert at.scale.shape == at.offset.shape == (2, 2, 250)
+    # Oracle decode of the atlas, restored with the token affine, tracks v.
+    tex, kinds = O.decode_blocks_fp16(at.blocks.reshape(-1, 16), bx, by)
+    assert np.all(kinds != 2)
+    bb, hh, rr, cc = at.blocks.shape[:4]
+    img = tex.reshape(bb, hh, rr, cc, by, bx, 4).transpose(0, 1, 2, 4, 3, 5, 6).reshape(bb, hh, rr * by, cc * bx, 4)
+    img = img[:, :, :250].astype(np.float32)
+    u = img[..., :d, 0] if layout == "scalar" else img[:, :, :, : d // 4].reshape(bb, hh, 250, d)
+    np.testing.assert_array_equal(u, at.normalized())
+    rec = R.restore_token(u, at.scale.astype(np.float32)[..., None], at.offset.astype(np.float32)[..., None])
+    # i.i.d. Gaussian V at 1.2-3.7 bits per value is coded coarsely: a
+    # sanity bound on the mean error relative to each token's range only.
+    span = at.scale.astype(np.float32)[..., None]
+    assert np.abs(rec - v).mean() < 0.2 * span.mean()
+    # Byte accounting: blocks + two fp16 per token.
+    counts = at.byte_counts()
+    assert counts["astc_blocks"] == at.blocks.size
+    assert counts["fp16_scales"] == counts["fp16_offsets"] == 2 * 2 * 250 * 2
+
+
+def test_default_tiles():
+    from astc_kv.gpu import default_tile, fp16_params, tile_for_splits
+    # c3 (48 sequences x kv heads, 240-token chunks): one chunk per split.
+    assert default_tile(16, 3, 8192, 240, 5) == 240
+    # c4 (64 sequences x kv heads, 72-token chunks): several chunks per split.
+    t = default_tile(8, 8, 32768, 72, 4)
+    assert t % 72 == 0 and 72 < t <= 8 * 72
+    # Tiny workloads: split for parallelism, in whole block rows, never above a chunk.
+    t = default_tile(1, 3, 384, 240, 5)
+    assert t % 5 == 0 and 16 <= t <= 240
+    assert tile_for_splits(2048, 8, 6, 64) == 258 and -(-2048 // 258) == 8
+    p = fp16_params(16, 3, 9, 8192, 64)
+    assert p.tile_tokens == 512 and p.splits == 16
