@@ -21,7 +21,16 @@
  *
  * Scope: 2D LDR blocks. HDR endpoint modes and HDR void-extent blocks decode
  * to the LDR error colour (magenta); so do reserved/invalid encodings.
- * Parity status per feature is listed in DESIGN.md.
+ *
+ * Pinned against astcenc's archived outputs (the reference's fixtures): 6x6
+ * blocks with endpoint modes 0/1, 1-4 partitions, reduced weight grids,
+ * trit/quint weights of 4-20 levels, and the UNORM16 -> FP16 rule. Pinned by
+ * closed forms: trit/quint block codes, integer-sequence bit counts,
+ * unquantisation levels, void extent, small-block partition coordinates.
+ * PARITY UNPINNED (no astcenc vector exists for them here; checked only by
+ * agreement with the separately written product decoders and by encoder
+ * round trips): endpoint modes 4-13 (RGB/RGBA, blue contraction, bit
+ * transfer), dual-plane blocks, footprints other than 6x6, and HDR modes.
  */
 #include <stdint.h>
 #include <string.h>
