@@ -91,20 +91,32 @@ def task_tokens(params: AkvAttnParams, astc: bool = True) -> int:
     return rc
 
 
-def default_tile(batch: int, kv_heads: int, tokens: int, chunk: int, block: int = 1, cu_count: int = 256) -> int:
+def default_tile(batch: int, kv_heads: int, tokens: int, chunk: int, block: int = 1, cu_count: int = 256,
+                 groups_per_cu: int = 3, overhead_tokens: int = 64) -> int:
     """Tokens per split (a multiple of `block`, the footprint height).
 
-    Small workloads (fewer chunks than CUs) get splits of about
-    tokens * batch * kv_heads / CUs tokens, at least 16, for parallelism. Otherwise
-    one chunk per split while that gives at most ~4 rounds of 3 resident
-    workgroups per CU; beyond that up to 8 chunks per split, which also cuts
-    the split-state traffic."""
+    * Fewer chunks than CUs: splits of about tokens * batch * kv_heads / CUs
+      tokens (at least 16) for parallelism.
+    * Up to 8 rounds of resident workgroups (groups_per_cu per CU): the tile
+      (at most one chunk) minimising rounds x (tile + overhead_tokens), i.e.
+      the time of the last workgroup to finish when each costs its tokens plus
+      a fixed overhead (a partial last round idles most CUs); the largest tile
+      within 3% of that minimum.
+    * More: several chunks per split (up to 8), which also cuts the
+      split-state traffic; the tail is small there."""
     seqs = batch * kv_heads
+    slots = groups_per_cu * cu_count
     total = seqs * -(-tokens // chunk)
     if total < cu_count:
         want = max(16, -(-tokens * seqs // cu_count))
         return min(chunk, -(-want // block) * block)
-    per_split = max(1, min(8, total // (4 * 3 * cu_count)))
+    if total <= 8 * slots:
+        tiles = range(chunk - chunk % block, 0, -block)
+        cost = {t: -(-seqs * -(-tokens // t) // slots) * (t + overhead_tokens) for t in tiles}
+        floor = min(cost.values())
+        # Within 3% of the best, fewer and longer workgroups win (less fixed work).
+        return max(t for t in tiles if cost[t] <= 1.03 * floor)
+    per_split = max(1, min(8, total // (4 * slots)))
     return per_split * chunk
 
 

@@ -52,8 +52,8 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 template <int D, int NCH>
 struct Cfg {
-    static constexpr int kMaxBlocks = 144;                       // blocks per chunk (header stage)
-    static constexpr int kMaxTok = D == 64 ? 256 : 128;          // tokens per chunk
+    static constexpr int kMaxBlocks = 160;                       // blocks per chunk (header stage)
+    static constexpr int kMaxTok = D == 64 ? 320 : 128;          // tokens per chunk
     static constexpr int kMaxTiles = kMaxTok / 16;
     static constexpr int kWaveTiles = kMaxTiles / kWaves;        // tiles per wave per chunk
     static constexpr int kRowLoads = D / 32;                     // K: 16-byte loads per lane per tile
@@ -295,8 +295,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
             load_k_tile<D>(kcur, kseq + size_t(c0) * D, 16 * wave, ntok, lane);
             load_k_tile<D>(knext, kseq + size_t(c0) * D, 16 * (wave + kWaves), ntok, lane);
         }
-        uint32_t so = 0;
-        if (!DUMP && tid < ntok) so = uint32_t(sseq[c0 + tid]) | (uint32_t(oseq[c0 + tid]) << 16);
+        // Per-token V scale | offset << 16 for up to two tokens per lane.
+        static_assert(C::kMaxTok <= 2 * kThreads, "two scale/offset tokens per lane");
+        uint32_t so[2] = {0, 0};
+        if constexpr (!DUMP) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int t = tid + i * kThreads;
+                if (t < ntok) so[i] = uint32_t(sseq[c0 + t]) | (uint32_t(oseq[c0 + t]) << 16);
+            }
+        }
         const uint4 raw_now = raw;
         if (c0 + CT < split_end) raw = load_block(bseq, cols, (c0 + CT) / by, chunk_blocks(c0 + CT), tid);
         // 2. Block headers, with the blocks sorted by decode-path class so that
@@ -310,7 +318,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
             rank = int(atomicAdd(&sh.key_count[key], 1u));
         }
         // Tokens past the chunk up to the tile edge get scale = offset = 0.
-        if (!DUMP && tid < 16 * ntiles) sh.so[tid] = so;
+        if constexpr (!DUMP) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                if (tid + i * kThreads < 16 * ntiles) sh.so[tid + i * kThreads] = so[i];
+        }
         __syncthreads();
         if (wave == 0) {   // exclusive scan of the class counts (kPathKeys == 64 lanes)
             const uint32_t c = sh.key_count[lane];

@@ -53,21 +53,21 @@ def c3(**kw):
 
 
 def test_chunk_tokens_follow_the_footprint(hip):
-    # 6x5 RGBA D64: 3 block columns, at most 144 blocks -> 48 block rows = 240 tokens.
-    assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=8190, splits=2)), 1) == 240
+    # 6x5 RGBA D64: 3 block columns, at most 160 blocks -> 53 block rows = 265 tokens.
+    assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=8190, splits=2)), 1) == 265
     # A split shorter than a chunk is one chunk.
     assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=35, splits=235)), 1) == 35
-    # 4x4 RGBA D64: 4 block columns -> 36 block rows = 144 tokens.
+    # 4x4 RGBA D64: 4 block columns -> 40 block rows = 160 tokens.
     p = c3(block_x=4, block_y=4, atlas_cols=4, atlas_rows=2048, tile_tokens=8192, splits=1)
-    assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 144
-    # Scalar 6x6 D64: 11 block columns -> 13 rows = 78 tokens.
+    assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 160
+    # Scalar 6x6 D64: 11 block columns -> 14 rows = 84 tokens.
     p = c3(layout=0, block_x=6, block_y=6, atlas_cols=11, atlas_rows=1366, tile_tokens=8196, splits=1)
-    assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 78
-    # D128 RGBA 4x4: 8 block columns -> 18 rows = 72 tokens.
+    assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 84
+    # D128 RGBA 4x4: 8 block columns -> 20 rows = 80 tokens.
     p = c3(dim=128, block_x=4, block_y=4, atlas_cols=8, atlas_rows=2048, tile_tokens=8192, splits=1)
-    assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 72
-    # FP16 control: whole 256-token chunks (128 for D128).
-    assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=8192, splits=1)), 0) == 256
+    assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 80
+    # FP16 control: whole 320-token chunks (128 for D128).
+    assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=8192, splits=1)), 0) == 320
     assert hip.akv_hip_task_tokens(ct.byref(c3(dim=128, tile_tokens=8192, splits=1)), 0) == 128
 
 

@@ -220,14 +220,19 @@ def test_atlas_layout_and_restore(layout, block, d):
 
 def test_default_tiles():
     from astc_kv.gpu import default_tile, fp16_params, tile_for_splits
-    # c3 (48 sequences x kv heads, 240-token chunks): one chunk per split.
-    assert default_tile(16, 3, 8192, 240, 5) == 240
-    # c4 (64 sequences x kv heads, 72-token chunks): several chunks per split.
-    t = default_tile(8, 8, 32768, 72, 4)
-    assert t % 72 == 0 and 72 < t <= 8 * 72
+    # c3 (48 sequence x kv-head pairs, 265-token chunks): whole chunks, 31 splits
+    # = 1488 workgroups, within two rounds of 3 per CU on 256 CUs.
+    t = default_tile(16, 3, 8192, 265, 5)
+    assert t == 265 and 48 * -(-8192 // t) <= 2 * 768
+    # 4x4 (160-token chunks): 52 splits would need 3.25 rounds; about 64 splits fill 4.
+    t = default_tile(16, 3, 8192, 160, 4)
+    assert 128 <= t <= 136 and 48 * -(-8192 // t) <= 4 * 768
+    # c4 (64 pairs, 80-token chunks, > 8 rounds): several chunks per split.
+    t = default_tile(8, 8, 32768, 80, 4)
+    assert t % 80 == 0 and 80 < t <= 8 * 80
     # Tiny workloads: split for parallelism, in whole block rows, never above a chunk.
-    t = default_tile(1, 3, 384, 240, 5)
-    assert t % 5 == 0 and 16 <= t <= 240
+    t = default_tile(1, 3, 384, 265, 5)
+    assert t % 5 == 0 and 16 <= t <= 265
     assert tile_for_splits(2048, 8, 6, 64) == 258 and -(-2048 // 258) == 8
     p = fp16_params(16, 3, 9, 8192, 64)
     assert p.tile_tokens == 512 and p.splits == 16
