@@ -11,15 +11,6 @@ namespace akv {
 
 namespace {
 
-// Per range: {plain bits, trit?, quint?}. Levels = (1 + 2*trit + 4*quint) << bits.
-struct IseRange {
-    uint8_t bits, trit, quint;
-};
-constexpr IseRange kIse[kNumRanges] = {
-    {1, 0, 0}, {0, 1, 0}, {2, 0, 0}, {0, 0, 1}, {1, 1, 0}, {3, 0, 0}, {1, 0, 1},
-    {2, 1, 0}, {4, 0, 0}, {2, 0, 1}, {3, 1, 0}, {5, 0, 0}, {3, 0, 1}, {4, 1, 0},
-    {6, 0, 0}, {4, 0, 1}, {5, 1, 0}, {7, 0, 0}, {5, 0, 1}, {6, 1, 0}, {8, 0, 0}};
-
 // Bit-pattern strings of the unquantisation "B" term, most significant bit
 // first; '0' is a zero bit and 'b'..'f' copy bit 1..5 of the ISE value's plain
 // part. Indexed by plain bit count (1..6 for colours, 1..3 for weights) with

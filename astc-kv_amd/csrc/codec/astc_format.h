@@ -17,6 +17,17 @@ constexpr int kMaxTexels = 64;     // footprints up to 8x8 (codec.py allows 4/6/
 constexpr int kNumRanges = 21;     // ISE ranges: 2,3,4,5,6,8,...,192,256 levels
 constexpr int kRange6 = 4;         // lowest range allowed for colour endpoints
 
+// Integer-sequence ranges, in the order of the ASTC range index: {plain bits,
+// trit?, quint?}; levels = (1 + 2*trit + 4*quint) << bits. Weight ranges are
+// indices 0..11, colour ranges 4..20.
+struct IseRange {
+    uint8_t bits, trit, quint;
+};
+inline constexpr IseRange kIse[kNumRanges] = {
+    {1, 0, 0}, {0, 1, 0}, {2, 0, 0}, {0, 0, 1}, {1, 1, 0}, {3, 0, 0}, {1, 0, 1},
+    {2, 1, 0}, {4, 0, 0}, {2, 0, 1}, {3, 1, 0}, {5, 0, 0}, {3, 0, 1}, {4, 1, 0},
+    {6, 0, 0}, {4, 0, 1}, {5, 1, 0}, {7, 0, 0}, {5, 0, 1}, {6, 1, 0}, {8, 0, 0}};
+
 // Packed block-mode descriptor (AkvTables::block_mode), 0 for an invalid or
 // reserved mode and for a void-extent selector.
 //   bits 0-3 grid width, 4-7 grid height, 8 dual plane, 9-12 weight range,

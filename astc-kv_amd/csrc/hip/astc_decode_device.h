@@ -22,6 +22,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "astc_format.h"
 
@@ -111,6 +112,224 @@ __device__ inline uint64_t stream_bits64_until(const uint32_t* s, int pos, int l
 
 __device__ inline uint32_t field64(uint64_t g, int pos, int len) {
     return uint32_t(g >> pos) & ((1u << len) - 1);
+}
+
+// --- Integer-sequence (BISE) unpacking specialised per range -----------------
+// The header stage dispatches each integer sequence on its range: the lanes of
+// a wave are walked in groups of equal range (readfirstlane loop), so inside a
+// group the range is a wave-uniform constant and every bit position below is a
+// compile-time constant of a 128-bit stream held in four registers.
+
+template <int I>
+using Idx = std::integral_constant<int, I>;
+
+template <int B, int E, typename F>
+__device__ __attribute__((always_inline)) inline void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(Idx<B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// Bits [P, P + N) of a 128-bit little-endian value (N <= 32); bits past the
+// 128 read as zero.
+template <int P, int N>
+__device__ inline uint32_t bits_at(const uint32_t (&s)[4]) {
+    static_assert(N >= 0 && N <= 32 && P >= 0, "field");
+    constexpr int w = P >> 5, o = P & 31;
+    if constexpr (N == 0 || P >= 128) {
+        return 0u;
+    } else if constexpr (P + N > 128) {
+        return bits_at<P, 128 - P>(s);
+    } else if constexpr (o + N <= 32) {
+        return N == 32 ? s[w] : __builtin_amdgcn_ubfe(s[w], uint32_t(o), uint32_t(N));
+    } else {
+        return __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(s[w + 1], s[w], uint32_t(o)), 0u, uint32_t(N));
+    }
+}
+
+// s >>= k (0 <= k < 32) and zero every bit at or past `end` (0 <= end).
+__device__ inline void shift_and_cut(uint32_t (&s)[4], uint32_t k, int end) {
+    s[0] = __builtin_amdgcn_alignbit(s[1], s[0], k);
+    s[1] = __builtin_amdgcn_alignbit(s[2], s[1], k);
+    s[2] = __builtin_amdgcn_alignbit(s[3], s[2], k);
+    s[3] = s[3] >> k;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int keep = end - 32 * i;
+        s[i] &= keep >= 32 ? ~0u : (keep <= 0 ? 0u : (1u << keep) - 1u);
+    }
+}
+
+// Sequence bits of `count` values of range R.
+template <int R>
+__device__ inline int ise_seq_bits(int count) {
+    constexpr akv::IseRange e = akv::kIse[R];
+    return count * e.bits + (e.trit ? (count * 8 + 4) / 5 : 0) + (e.quint ? (count * 7 + 2) / 3 : 0);
+}
+
+constexpr int ise_seq_bits_c(int count, int r) {
+    return count * akv::kIse[r].bits + (akv::kIse[r].trit ? (count * 8 + 4) / 5 : 0) +
+           (akv::kIse[r].quint ? (count * 7 + 2) / 3 : 0);
+}
+
+// Largest value count (<= cap) of range r whose sequence fits in `budget` bits.
+constexpr int ise_max_values(int r, int cap, int budget) {
+    int v = cap;
+    while (v > 0 && ise_seq_bits_c(v, r) > budget) --v;
+    return v;
+}
+
+// Values 0 .. V-1 of an integer sequence of range R starting at bit 0 of s:
+// emit(Idx<j>, value) with value = digit << bits | plain bits. Values past the
+// real sequence are garbage (bits past its end must already be zero, since a
+// truncated trit/quint group decodes with its missing bits as zero).
+template <int R, int V, typename Emit>
+__device__ __attribute__((always_inline)) inline void ise_unpack(const uint32_t (&s)[4], const LdsTables& L, Emit&& emit) {
+    constexpr akv::IseRange e = akv::kIse[R];
+    constexpr int n = e.bits;
+    if constexpr (e.trit) {
+        constexpr int gb = 5 * n + 8;
+        static_for<0, (V + 4) / 5>([&](auto gi) {
+            constexpr int p = decltype(gi)::value * gb;
+            uint32_t T;
+            if constexpr (n == 0) {
+                T = bits_at<p, 8>(s);
+            } else {
+                T = bits_at<p + n, 2>(s) | bits_at<p + 2 * n + 2, 2>(s) << 2 | bits_at<p + 3 * n + 4, 1>(s) << 4 |
+                    bits_at<p + 4 * n + 5, 2>(s) << 5 | bits_at<p + 5 * n + 7, 1>(s) << 7;
+            }
+            const uint32_t dig = L.trit[T];
+            constexpr int moff[5] = {0, n + 2, 2 * n + 4, 3 * n + 5, 4 * n + 7};
+            static_for<0, 5>([&](auto ji) {
+                constexpr int j = decltype(ji)::value, v = 5 * decltype(gi)::value + j;
+                if constexpr (v < V)
+                    emit(Idx<v>{}, (((dig >> (2 * j)) & 3u) << n) | bits_at<p + moff[j], n>(s));
+            });
+        });
+    } else if constexpr (e.quint) {
+        constexpr int gb = 3 * n + 7;
+        static_for<0, (V + 2) / 3>([&](auto gi) {
+            constexpr int p = decltype(gi)::value * gb;
+            uint32_t Q;
+            if constexpr (n == 0) {
+                Q = bits_at<p, 7>(s);
+            } else {
+                Q = bits_at<p + n, 3>(s) | bits_at<p + 2 * n + 3, 2>(s) << 3 | bits_at<p + 3 * n + 5, 2>(s) << 5;
+            }
+            const uint32_t dig = L.quint[Q];
+            constexpr int moff[3] = {0, n + 3, 2 * n + 5};
+            static_for<0, 3>([&](auto ji) {
+                constexpr int j = decltype(ji)::value, v = 3 * decltype(gi)::value + j;
+                if constexpr (v < V)
+                    emit(Idx<v>{}, (((dig >> (3 * j)) & 7u) << n) | bits_at<p + moff[j], n>(s));
+            });
+        });
+    } else {
+        static_for<0, V>([&](auto ji) { emit(ji, bits_at<decltype(ji)::value * n, n>(s)); });
+    }
+}
+
+// Colour values of range R (4..20): at most 18, and never more than fit in the
+// 111 bits after the 17-bit header.
+template <int R>
+__device__ __attribute__((always_inline)) inline void colour_values(const uint32_t (&s)[4], const LdsTables& L,
+                                                                    uint8_t* cv) {
+    constexpr int V = ise_max_values(R, 18, 111);
+    ise_unpack<R, V>(s, L, [&](auto ji, uint32_t v) { cv[decltype(ji)::value] = L.color_unq[R][v]; });
+}
+
+// Weight fields of trit/quint range R as plain nb-bit fields (nb = bits + 2
+// for trits, bits + 3 for quints), field j at bit j * nb of q (five words).
+// At most 64 weights, never more than fit in 96 bits.
+template <int R>
+__device__ __attribute__((always_inline)) inline void weight_fields(const uint32_t (&s)[4], const LdsTables& L,
+                                                                    uint32_t (&q)[5]) {
+    constexpr akv::IseRange e = akv::kIse[R];
+    constexpr int nb = e.bits + (e.trit ? 2 : 3);
+    constexpr int V = ise_max_values(R, 64, 96);
+    static_assert(V * nb <= 160, "weight fields fit five words");
+#pragma unroll
+    for (int i = 0; i < 5; ++i) q[i] = 0;
+    ise_unpack<R, V>(s, L, [&](auto ji, uint32_t v) {
+        constexpr int P = decltype(ji)::value * nb, w = P >> 5, o = P & 31;
+        q[w] |= v << o;
+        if constexpr (o + nb > 32) q[w + 1] |= v >> (32 - o);
+    });
+}
+
+// Colour integer sequence of this lane's block: range `crange`, `nv` values
+// from bit `start` of the block `blk` (four words in LDS) -> cv[0..].
+__device__ inline void decode_colour_values(const uint32_t* blk, int start, int crange, int nv, const LdsTables& L,
+                                            uint8_t* cv) {
+    const uint4 b4 = *reinterpret_cast<const uint4*>(blk);
+    while (true) {
+        const int r = __builtin_amdgcn_readfirstlane(crange);
+        if (crange == r) {
+            uint32_t s[4] = {b4.x, b4.y, b4.z, b4.w};
+            auto run = [&](auto ri) {
+                constexpr int R = decltype(ri)::value;
+                shift_and_cut(s, uint32_t(start), ise_seq_bits<R>(nv));
+                colour_values<R>(s, L, cv);
+            };
+            switch (r) {
+                case 4: run(Idx<4>{}); break;
+                case 5: run(Idx<5>{}); break;
+                case 6: run(Idx<6>{}); break;
+                case 7: run(Idx<7>{}); break;
+                case 8: run(Idx<8>{}); break;
+                case 9: run(Idx<9>{}); break;
+                case 10: run(Idx<10>{}); break;
+                case 11: run(Idx<11>{}); break;
+                case 12: run(Idx<12>{}); break;
+                case 13: run(Idx<13>{}); break;
+                case 14: run(Idx<14>{}); break;
+                case 15: run(Idx<15>{}); break;
+                case 16: run(Idx<16>{}); break;
+                case 17: run(Idx<17>{}); break;
+                case 18: run(Idx<18>{}); break;
+                case 19: run(Idx<19>{}); break;
+                default: run(Idx<20>{}); break;
+            }
+            break;
+        }
+    }
+}
+
+// Weight integer sequence of this lane's block (range `wrange`, `wbits` bits
+// of the bit-reversed block `rev`) -> nb-bit fields in q. Plain ranges are
+// already nb-bit fields.
+__device__ inline void decode_weight_fields(const uint32_t* rev, int wrange, int wbits, const LdsTables& L,
+                                            uint32_t (&q)[5]) {
+    const uint4 r4 = *reinterpret_cast<const uint4*>(rev);
+    while (true) {
+        const int r = __builtin_amdgcn_readfirstlane(wrange);
+        if (wrange == r) {
+            uint32_t s[4] = {r4.x, r4.y, r4.z, r4.w};
+            auto run = [&](auto ri) {
+                constexpr int R = decltype(ri)::value;
+                shift_and_cut(s, 0u, wbits);
+                weight_fields<R>(s, L, q);
+            };
+            switch (r) {
+                case 1: run(Idx<1>{}); break;
+                case 3: run(Idx<3>{}); break;
+                case 4: run(Idx<4>{}); break;
+                case 6: run(Idx<6>{}); break;
+                case 7: run(Idx<7>{}); break;
+                case 9: run(Idx<9>{}); break;
+                case 10: run(Idx<10>{}); break;
+                default:   // plain binary: the fields are the reversed stream itself
+                    q[0] = r4.x;
+                    q[1] = r4.y;
+                    q[2] = r4.z;
+                    q[3] = r4.w;
+                    q[4] = 0;
+                    break;
+            }
+            break;
+        }
+    }
 }
 
 __device__ inline int clamp255(int v) { return v < 0 ? 0 : (v > 255 ? 255 : v); }
@@ -284,9 +503,9 @@ __device__ inline void stash_block(BlockDesc<NCH>& d, uint4 raw, uint4 pw) {
 }
 
 // Decode-path class of a block, 0..kPathKeys-1: blocks of one class take the
-// same branches through decode_header (weight and colour integer-sequence
-// kinds, partition count), so sorting a chunk's blocks by class before the
-// header stage keeps the lanes of a wave on one path. Constant blocks (void
+// same branches through decode_header (weight range, partition count and
+// colour range, up to collisions of the fold), so sorting a chunk's blocks by
+// class before the header stage keeps the lanes of a wave on one path. Constant blocks (void
 // extent, reserved or invalid modes) are class kPathKeys - 1.
 constexpr int kPathKeys = 64;
 
@@ -295,8 +514,6 @@ __device__ inline int block_path_key(uint4 raw, const LdsTables& L) {
     const uint32_t md = L.block_mode[mode];
     const int parts = int((raw.x >> 11) & 3) + 1;
     if ((mode & 0x1FF) == 0x1FC || !md || (akv::mode_dual(md) && parts == 4)) return kPathKeys - 1;
-    const uint32_t wise = L.ise[akv::mode_range(md)];
-    const int wkind = (wise >> 8) & 3;   // 0 plain, 1 trit, 2 quint
     // Colour range as decode_header derives it.
     int below = 128 - int(akv::mode_wbits(md)) - (akv::mode_dual(md) ? 2 : 0);
     uint32_t cems;
@@ -319,8 +536,8 @@ __device__ inline int block_path_key(uint4 raw, const LdsTables& L) {
     const int avail = below - (parts == 1 ? 17 : 29);
     const int crange = (pairs <= 9 && avail > 0) ? int(L.color_range[pairs][min(avail, 127)]) : -1;
     if (crange < akv::kRange6) return kPathKeys - 1;
-    const int ckind = (L.ise[crange] >> 8) & 3;
-    return wkind | (ckind << 2) | ((parts - 1) << 4);
+    // (weight range, partition count, colour range) folded onto 63 classes.
+    return ((int(akv::mode_range(md)) * 4 + parts - 1) * 17 + crange - akv::kRange6) % (kPathKeys - 1);
 }
 
 // The partition-pattern words a block selects (any 128-bit value selects an
@@ -400,114 +617,19 @@ __device__ __attribute__((always_inline)) inline void decode_header(const LdsTab
     }
     const uint4 pw = *reinterpret_cast<const uint4*>(d.tab + 4);
 
-    // Colour integer sequence -> unquantised colour bytes. The loops are
-    // unrolled and branch-free so that their LDS reads issue together: values
-    // and groups past the sequence read bits of this block's own record
-    // (garbage, at most 210 bits in) and their bytes are never used.
-    {
-        const int nv = 2 * pairs;
-        const uint32_t ise = L.ise[crange];
-        const int n = int(ise & 0xFF);
-        const uint8_t* unq = L.color_unq[crange];
-        if (ise & 0x100) {
-            const int end = color_start + nv * n + (nv * 8 + 4) / 5;
-            const int moff[5] = {0, n + 2, 2 * n + 4, 3 * n + 5, 4 * n + 7};
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int pos = color_start + g * (5 * n + 8);
-                const uint64_t G = stream_bits64_until(blk, pos, 5 * n + 8, end);
-                const uint32_t T = field64(G, n, 2) | field64(G, 2 * n + 2, 2) << 2 | field64(G, 3 * n + 4, 1) << 4 |
-                                   field64(G, 4 * n + 5, 2) << 5 | field64(G, 5 * n + 7, 1) << 7;
-                const uint32_t dig = L.trit[T];
-#pragma unroll
-                for (int j = 0; j < 5; ++j)
-                    if (5 * g + j < 18) cv[5 * g + j] = unq[(((dig >> (2 * j)) & 3) << n) | field64(G, moff[j], n)];
-            }
-        } else if (ise & 0x200) {
-            const int end = color_start + nv * n + (nv * 7 + 2) / 3;
-            const int moff[3] = {0, n + 3, 2 * n + 5};
-#pragma unroll
-            for (int g = 0; g < 6; ++g) {
-                const int pos = color_start + g * (3 * n + 7);
-                const uint32_t G = stream_bits_until(blk, pos, 3 * n + 7, end);   // at most 22 bits
-                const uint32_t Q = __builtin_amdgcn_ubfe(G, n, 3) | __builtin_amdgcn_ubfe(G, 2 * n + 3, 2) << 3 |
-                                   __builtin_amdgcn_ubfe(G, 3 * n + 5, 2) << 5;
-                const uint32_t dig = L.quint[Q];
-#pragma unroll
-                for (int j = 0; j < 3; ++j)
-                    cv[3 * g + j] = unq[(((dig >> (3 * j)) & 7) << n) | __builtin_amdgcn_ubfe(G, moff[j], n)];
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 18; ++j) cv[j] = unq[stream_bits(blk, color_start + j * n, n)];
-        }
-    }
+    // Colour integer sequence -> unquantised colour bytes.
+    decode_colour_values(blk, color_start, crange, 2 * pairs, L, cv);
 
     // Weights: the integer sequence runs from bit 127 downwards, so in the
-    // bit-reversed block it starts at bit 0. Unpacked to nb-bit fields, one
-    // appended chunk per group (a group is at most 23 bits). Unrolled and
-    // branch-free like the colour loops: at most 96 weight bits make at most
-    // 12 trit groups or 14 quint groups.
+    // bit-reversed block it starts at bit 0; unpacked to nb-bit fields.
     const int wrange = int(akv::mode_range(md));
-    const uint32_t wise = L.ise[wrange];
-    const int n = int(wise & 0xFF);
-    const int nw = int(akv::mode_gw(md) * akv::mode_gh(md)) << (dual ? 1 : 0);
-    int nb = n;
-    if (wise & 0x300) {
-        FieldWriter fw{d.qw, 0u, 0, 0};
-        if (wise & 0x100) {
-            nb = n + 2;
-            const int moff[5] = {0, n + 2, 2 * n + 4, 3 * n + 5, 4 * n + 7};
+    const uint32_t wi = L.ise[wrange];
+    const int nb = int(wi & 0xFF) + ((wi & 0x100) ? 2 : (wi & 0x200) ? 3 : 0);
+    {
+        uint32_t q[5];
+        decode_weight_fields(rev, wrange, wbits, L, q);
 #pragma unroll
-            for (int g = 0; g < 12; ++g) {
-                const int pos = g * (5 * n + 8);
-                const uint32_t G = stream_bits_until(rev, pos, 5 * n + 8, wbits);
-                const uint32_t T = __builtin_amdgcn_ubfe(G, n, 2) | __builtin_amdgcn_ubfe(G, 2 * n + 2, 2) << 2 |
-                                   __builtin_amdgcn_ubfe(G, 3 * n + 4, 1) << 4 |
-                                   __builtin_amdgcn_ubfe(G, 4 * n + 5, 2) << 5 |
-                                   __builtin_amdgcn_ubfe(G, 5 * n + 7, 1) << 7;
-                const uint32_t dig = L.trit[T];   // five 2-bit trits: the fields themselves when n == 0
-                uint32_t chunk = dig;
-                if (n > 0) {
-                    chunk = 0;
-#pragma unroll
-                    for (int j = 0; j < 5; ++j)
-                        chunk |= ((((dig >> (2 * j)) & 3) << n) | __builtin_amdgcn_ubfe(G, moff[j], n)) << (j * nb);
-                }
-                const int len = min(max(nw - 5 * g, 0), 5) * nb;
-                fw.put(__builtin_amdgcn_ubfe(chunk, 0, len), len);
-            }
-        } else {
-            nb = n + 3;
-            const int moff[3] = {0, n + 3, 2 * n + 5};
-#pragma unroll
-            for (int g = 0; g < 14; ++g) {
-                const int pos = g * (3 * n + 7);
-                const uint32_t G = stream_bits_until(rev, pos, 3 * n + 7, wbits);
-                const uint32_t Q = __builtin_amdgcn_ubfe(G, n, 3) | __builtin_amdgcn_ubfe(G, 2 * n + 3, 2) << 3 |
-                                   __builtin_amdgcn_ubfe(G, 3 * n + 5, 2) << 5;
-                const uint32_t dig = L.quint[Q];  // three 3-bit quints: the fields themselves when n == 0
-                uint32_t chunk = dig;
-                if (n > 0) {
-                    chunk = 0;
-#pragma unroll
-                    for (int j = 0; j < 3; ++j)
-                        chunk |= ((((dig >> (3 * j)) & 7) << n) | __builtin_amdgcn_ubfe(G, moff[j], n)) << (j * nb);
-                }
-                const int len = min(max(nw - 3 * g, 0), 3) * nb;
-                fw.put(__builtin_amdgcn_ubfe(chunk, 0, len), len);
-            }
-        }
-        fw.finish();
-    } else {
-        // Plain binary fields are nb-bit fields of the reversed stream already;
-        // fields past the weight count are never read.
-        const uint4 r4 = *reinterpret_cast<const uint4*>(rev);
-        d.qw[0] = r4.x;
-        d.qw[1] = r4.y;
-        d.qw[2] = r4.z;
-        d.qw[3] = r4.w;
-        d.qw[4] = 0;
+        for (int i = 0; i < 5; ++i) d.qw[i] = q[i];
     }
 
     // Endpoints per partition -> endpoint pairs, or the texel table. (The
@@ -529,12 +651,12 @@ __device__ __attribute__((always_inline)) inline void decode_header(const LdsTab
         }
         k += 2 * ((cem >> 2) + 1);
         if (table) {
-            // Entries past this partition's row are rewritten by the next
-            // partition or unused; none lies past the table.
+            // One row of `levels` entries per partition (parts * levels fits).
 #pragma unroll
-            for (int q = 0; q < BlockDesc<NCH>::kTabEntries; ++q)
-                if (p * levels + q < BlockDesc<NCH>::kTabEntries)
-                    put_entry<NCH>(d.tab, p * levels + q, ep, weight_pair(L.weight_unq[wrange][q]));
+            for (int q = 0; q < BlockDesc<NCH>::kTabEntries; ++q) {
+                if (q >= levels) break;
+                put_entry<NCH>(d.tab, p * levels + q, ep, weight_pair(L.weight_unq[wrange][q]));
+            }
         } else {
 #pragma unroll
             for (int ch = 0; ch < NCH; ++ch) d.ep[p][ch] = ep[ch];

@@ -85,126 +85,271 @@ __device__ inline int pv_channel(int mb, int row) {
     else return 16 * mb + row;
 }
 
-// Q as the B operand of Q.K^T, split into fp16 high and low parts. k-step ks
-// covers dims 32*(ks/2) + 8*g + 4*(ks%2) + j, matching the K row loads.
+// Grouped attention. One 16x16x16 MFMA output holds TPG 16-token tiles x Gs
+// head slots: rows r = t * Gs + h (tile t of the group, query head h), so that
+// for G <= 4 the softmax runs on 4 head slots instead of the 16 columns of one
+// tile. Q is block-diagonal (row r sees only the K rows of tile t), P likewise
+// for P.V; the MFMA count is the same as one tile at a time.
+template <int G>
+struct Grp {
+    static constexpr int Gs = G <= 4 ? 4 : 8;   // head slots per tile
+    static constexpr int TPG = 16 / Gs;          // tiles per group
+};
+
+// Q as the B operand of the block-diagonal S^T = K.Q^T, split into fp16 high
+// and low parts, kept in LDS (the same for every wave): qs[2 * ks + part][lane]
+// for lane (column r, g) holds head r % Gs, dims 32*(ks/2) + 8*g + 4*(ks%2) + j
+// (j = 0..3), matching the K row loads. Written by the first wave.
 template <int D, int G>
-__device__ inline void load_q(const float* __restrict__ qrow, float qscale, int n16, int g, half4* qhi, half4* qlo) {
-#pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float v = n16 < G ? qrow[size_t(n16) * D + 32 * (ks / 2) + 8 * g + 4 * (ks % 2) + j] * qscale : 0.0f;
-            const _Float16 hi = _Float16(v);
-            qhi[ks][j] = hi;
-            qlo[ks][j] = _Float16(v - float(hi));
-        }
-}
-
-// K rows of one 16-token tile in the MFMA A-operand layout: lane holds token
-// t0 + lane % 16, dims 32 * L + 8 * (lane / 16) .. + 7; tokens at or past ntok
-// read as zero.
-template <int D>
-__device__ inline void load_k_tile(uint4* r, const uint16_t* __restrict__ seq, int t0, int ntok, int lane) {
-    const int tok = t0 + (lane & 15), g = lane >> 4;
-#pragma unroll
-    for (int L = 0; L < D / 32; ++L)
-        r[L] = tok < ntok ? *reinterpret_cast<const uint4*>(seq + size_t(tok) * D + 32 * L + 8 * g) : uint4{0, 0, 0, 0};
-}
-
-// One tile of attention for one wave: scores from the K rows, online softmax
-// update, and O += V^T P with the V operands va (one half4 per row block).
-// `valid` = tokens of the tile that exist; so4 = per-token (scale | offset<<16)
-// of this lane's four score rows (AFFINE only).
-template <int D, bool AFFINE>
-__device__ inline void attend_tile(const uint4* kr, const half4* qhi, const half4* qlo, const half4* va, uint4 so4,
-                                   int valid, int g, float& m_run, float& l_run, float& off_run, floatx4* o) {
-    floatx4 s = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+__device__ inline void store_q(const float* __restrict__ qrow, float qscale, uint2* qs) {
+    const int lane = threadIdx.x & 63, n16 = lane & 15, g = lane >> 4;
+    const int h = n16 % Grp<G>::Gs;
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
-        const uint4 kk = kr[ks / 2];
-        const half4 ka = __builtin_bit_cast(half4, (ks & 1) ? uint2{kk.z, kk.w} : uint2{kk.x, kk.y});
-        s = __builtin_amdgcn_mfma_f32_16x16x16f16(ka, qhi[ks], s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_16x16x16f16(ka, qlo[ks], s, 0, 0, 0);
+        half4 hi, lo;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float v = h < G ? qrow[size_t(h) * D + 32 * (ks / 2) + 8 * g + 4 * (ks % 2) + j] * qscale : 0.0f;
+            hi[j] = _Float16(v);
+            lo[j] = _Float16(v - float(hi[j]));
+        }
+        qs[(2 * ks) * 64 + lane] = __builtin_bit_cast(uint2, hi);
+        qs[(2 * ks + 1) * 64 + lane] = __builtin_bit_cast(uint2, lo);
     }
-    float mt = -INFINITY;
+}
+
+__device__ inline half4 masked(uint2 v, uint32_t m) { return __builtin_bit_cast(half4, uint2{v.x & m, v.y & m}); }
+
+// Cross-lane all-reductions over the lanes whose index agrees with this
+// lane's in the bits below `from` (a power of two, 4 .. 32): DPP row rotations
+// inside each 16-lane row, then the gfx950 row-swap moves across rows (with
+// both operands the same register, the two results of a swap hold the two
+// halves being combined, so op(first, second) is already the all-reduce).
+// Vector elements are copied to scalars before __builtin_bit_cast: applied to
+// an element of an ext_vector_type value directly it reads element 0.
+template <typename Op>
+__device__ inline float lane_allreduce(float v, int from, Op op) {
+    auto f32 = [](uint32_t u) { return __builtin_bit_cast(float, u); };
+    auto u32 = [](float f) { return __builtin_bit_cast(uint32_t, f); };
+    if (from <= 4) v = op(v, f32(__builtin_amdgcn_mov_dpp(int(u32(v)), 0x124, 0xF, 0xF, false)));
+    if (from <= 8) v = op(v, f32(__builtin_amdgcn_mov_dpp(int(u32(v)), 0x128, 0xF, 0xF, false)));
+    if (from <= 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(u32(v), u32(v), false, false);
+        const uint32_t a = r[0], b = r[1];
+        v = op(f32(a), f32(b));
+    }
+    const auto r = __builtin_amdgcn_permlane32_swap(u32(v), u32(v), false, false);
+    const uint32_t a = r[0], b = r[1];
+    return op(f32(a), f32(b));
+}
+struct MaxOp { __device__ float operator()(float a, float b) const { return fmaxf(a, b); } };
+struct AddOp { __device__ float operator()(float a, float b) const { return a + b; } };
+
+// A lane mask the optimizer cannot see through (keeps selects on it as plain
+// bit operations instead of dynamic vector indexing).
+__device__ inline uint32_t opaque_mask(bool c) {
+    uint32_t m = c ? ~0u : 0u;
+    asm volatile("" : "+v"(m));
+    return m;
+}
+
+// Buffer resource over `bytes` bytes from `base` (raw, stride 0): loads past
+// the end return zero without touching memory.
+__device__ inline __amdgpu_buffer_rsrc_t seq_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
+}
+
+// K rows of one 16-token tile as the A operand (lane (token, g) holds dims
+// 32 * L + 8 * g .. + 7 in kreg[L]); rs covers the tokens that exist, so rows
+// past them read as zero.
+template <int D>
+__device__ inline void load_k_tile(uint4* r, __amdgpu_buffer_rsrc_t rs, int t0, int lane) {
+    const uint32_t tok = uint32_t(t0 + (lane & 15)), g = uint32_t(lane >> 4);
+#pragma unroll
+    for (int L = 0; L < D / 32; ++L) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, 2 * (tok * D + 32 * L + 8 * g), 0, 0);
+        r[L] = uint4{v[0], v[1], v[2], v[3]};
+    }
+}
+
+// Softmax state of one wave. In the row layout (lane (r, g): tile r / Gs,
+// head r % Gs) m is the head's running maximum (log2 units) and l, off are
+// this lane's partial sums; o[mb] are the P.V accumulators in the MFMA output
+// layout (lane (channel, g): rows 4g .. 4g+3).
+template <int D>
+struct AttnState {
+    float m, l, off;
+    floatx4 o[D / 16];
+};
+
+// One group of up to TPG tiles (ng of them exist) starting at chunk token tb0:
+// kreg[t * D/32 + L] are tile t's K rows; vtile(t, va) produces tile t's V
+// operands (lane (channel, g): tokens 4g..4g+3 of the tile, one half4 per
+// 16-channel block). so: per-token scale | offset << 16 for the chunk (AFFINE).
+template <int D, int G, bool AFFINE, typename VTile>
+__device__ __attribute__((always_inline)) inline void attend_group(const uint4* kreg, const uint2* qs, int ng, int tb0,
+                                                                   int ntok, const uint32_t* so, int so_cap,
+                                                                   AttnState<D>& st, VTile&& vtile) {
+    constexpr int Gs = Grp<G>::Gs, TPG = Grp<G>::TPG;
+    const int lane = threadIdx.x & 63, n16 = lane & 15, g = lane >> 4;
+    const int rt = n16 / Gs, h = n16 % Gs;   // this lane's row of S and P: tile, head
+    // S^T = K . Q^T per tile, K rows as the A operand and Q as the B operand:
+    // output lane (column r, g) of tile t holds head r % Gs's scores for tokens
+    // 4g .. 4g+3 of tile t, the layout P needs as an A operand. Lane (r, g)
+    // keeps tile r / Gs. The Q operands are read from LDS here rather than
+    // kept in registers (the asm statement keeps the compiler from hoisting
+    // them out of the loop).
+    asm volatile("" ::: "memory");
+    floatx4 sacc[TPG];
+#pragma unroll
+    for (int t = 0; t < TPG; ++t) sacc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+        const half4 qh = __builtin_bit_cast(half4, qs[(2 * ks) * 64 + lane]);
+        const half4 ql = __builtin_bit_cast(half4, qs[(2 * ks + 1) * 64 + lane]);
+#pragma unroll
+        for (int t = 0; t < TPG; ++t) {
+            if (t >= ng) break;
+            const uint4 kk = kreg[t * (D / 32) + ks / 2];
+            const half4 ka = __builtin_bit_cast(half4, (ks & 1) ? uint2{kk.z, kk.w} : uint2{kk.x, kk.y});
+            sacc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(ka, qh, sacc[t], 0, 0, 0);
+            sacc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(ka, ql, sacc[t], 0, 0, 0);
+        }
+    }
+    uint32_t tmask[TPG];   // lane keeps tile t
+#pragma unroll
+    for (int t = 0; t < TPG; ++t) tmask[t] = opaque_mask(rt == t);
+    float x[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        if (4 * g + i >= valid) s[i] = -INFINITY;
-        mt = fmaxf(mt, s[i]);
+        uint32_t xb = 0;
+#pragma unroll
+        for (int t = 0; t < TPG; ++t) {
+            const float e = sacc[t][i];
+            xb |= __builtin_bit_cast(uint32_t, e) & tmask[t];
+        }
+        x[i] = __builtin_bit_cast(float, xb);
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float m_new = fmaxf(m_run, mt);   // finite: token 0 of the tile exists
-    // v_exp_f32 directly: exact to ~1 ulp for normal results; results below
-    // 2^-126 (weights under 1e-38 of the running maximum) flush to zero.
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    m_run = m_new;
+    const int tb = tb0 + 16 * rt + 4 * g;   // chunk token of x[0]
+    float mt = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (h < G && rt < ng && tb + i < ntok) mt = fmaxf(mt, x[i]);
+    mt = lane_allreduce(mt, Gs, MaxOp{});
+    const float m_new = fmaxf(st.m, mt);
+    const float mref = m_new == -INFINITY ? 0.0f : m_new;   // rows with no token yet
+    // v_exp_f32 directly: ~1 ulp for normal results; results below 2^-126 of
+    // the running maximum flush to zero.
+    const float alpha = __builtin_amdgcn_exp2f(st.m - mref);
+    st.m = m_new;
+    uint4 so4 = uint4{0x3C00u, 0x3C00u, 0x3C00u, 0x3C00u};   // scale 1, offset 0
+    if constexpr (AFFINE) so4 = *reinterpret_cast<const uint4*>(&so[min(tb, so_cap - 4)]);
     const uint32_t sov[4] = {so4.x, so4.y, so4.z, so4.w};
     float psum = 0.0f, poff = 0.0f;
     half4 phi, plo;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float pr = __builtin_amdgcn_exp2f(s[i] - m_new);
+        const bool ok = h < G && rt < ng && tb + i < ntok;
+        const float pr = ok ? __builtin_amdgcn_exp2f(x[i] - mref) : 0.0f;
         psum += pr;
         float pv = pr;
-        if constexpr (AFFINE) {
-            pv = pr * half_to_float(uint16_t(sov[i]));
-            poff = fmaf(pr, half_to_float(uint16_t(sov[i] >> 16)), poff);
+        if constexpr (AFFINE) {   // rows or tokens that do not exist: scale = offset = 0
+            const uint32_t sv = ok ? sov[i] : 0u;
+            pv = pr * half_to_float(uint16_t(sv));
+            poff = fmaf(pr, half_to_float(uint16_t(sv >> 16)), poff);
         }
-        const _Float16 h = _Float16(pv);
-        phi[i] = h;
-        plo[i] = _Float16(pv - float(h));
+        const _Float16 hh = _Float16(pv);
+        phi[i] = hh;
+        plo[i] = _Float16(pv - float(hh));
     }
-    l_run = fmaf(l_run, alpha, psum);
-    off_run = fmaf(off_run, alpha, poff);
+    st.l = fmaf(st.l, alpha, psum);
+    st.off = fmaf(st.off, alpha, poff);
+    // Rescale the accumulators by their row's alpha when any maximum moved:
+    // output row 4g + i has head (4g + i) % Gs, whose alpha lane h = row holds.
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+        float ar[4];
 #pragma unroll
-    for (int mb = 0; mb < D / 16; ++mb) {
-        o[mb] *= alpha;
-        o[mb] = __builtin_amdgcn_mfma_f32_16x16x16f16(va[mb], phi, o[mb], 0, 0, 0);
-        o[mb] = __builtin_amdgcn_mfma_f32_16x16x16f16(va[mb], plo, o[mb], 0, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (Gs == 4) {
+                ar[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), i));
+            } else {
+                const float a0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), i));
+                const float a1 =
+                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), 4 + i));
+                ar[i] = (g & 1) ? a1 : a0;
+            }
+        }
+#pragma unroll
+        for (int mb = 0; mb < D / 16; ++mb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) st.o[mb][i] *= ar[i];
+    }
+    const uint2 phib = __builtin_bit_cast(uint2, phi), plob = __builtin_bit_cast(uint2, plo);
+    // O += Pbd . V per tile.
+#pragma unroll
+    for (int t = 0; t < TPG; ++t) {
+        if (t >= ng) break;
+        half4 va[D / 16];
+        vtile(t, va);
+        const half4 ah = masked(phib, tmask[t]), al = masked(plob, tmask[t]);
+#pragma unroll
+        for (int mb = 0; mb < D / 16; ++mb) {
+            st.o[mb] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, va[mb], st.o[mb], 0, 0, 0);
+            st.o[mb] = __builtin_amdgcn_mfma_f32_16x16x16f16(al, va[mb], st.o[mb], 0, 0, 0);
+        }
     }
 }
 
 struct WaveStats {
-    float wm[kWaves][16], wl[kWaves][16], wo[kWaves][16];
+    float wm[kWaves][kMaxG], wl[kWaves][kMaxG], wo[kWaves][kMaxG];
 };
 
-// Combine the four waves' states into this split's state (partial, stats).
-// comb: [kWaves][D][kMaxG] floats in LDS, free for this use.
+// Combine: each wave sums its rows over the group's tiles and over lanes, then
+// the four waves' states merge into this split's (partial, stats). comb:
+// [kWaves][D][kMaxG] floats in LDS, free for this use.
 template <int D, int NCH, int G>
-__device__ inline void combine_waves(float* comb, WaveStats& ws, const floatx4* o, float m_run, float l_run,
-                                     float off_run, float* __restrict__ partial, float2* __restrict__ stats,
-                                     size_t qh0, int S, int split) {
+__device__ inline void combine_waves(float* comb, WaveStats& ws, AttnState<D>& st, float* __restrict__ partial,
+                                     float2* __restrict__ stats, size_t qh0, int S, int split) {
+    constexpr int Gs = Grp<G>::Gs;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n16 = lane & 15, g = lane >> 4;
-    l_run += __shfl_xor(l_run, 16, 64);
-    l_run += __shfl_xor(l_run, 32, 64);
-    off_run += __shfl_xor(off_run, 16, 64);
-    off_run += __shfl_xor(off_run, 32, 64);
-    if (n16 < G) {
+    // Row partial sums over the tiles of a group and all lanes of a head.
+    st.l = lane_allreduce(st.l, Gs, AddOp{});
+    st.off = lane_allreduce(st.off, Gs, AddOp{});
+    // Accumulator rows 4g + i = (tile, head): sum over the tiles.
+#pragma unroll
+    for (int mb = 0; mb < D / 16; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            st.o[mb][i] = lane_allreduce(st.o[mb][i], 16 * (Gs / 4), AddOp{});
+        }
+    if (g < Gs / 4) {
 #pragma unroll
         for (int mb = 0; mb < D / 16; ++mb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) comb[(wave * D + pv_channel<NCH>(mb, 4 * g + i)) * kMaxG + n16] = o[mb][i];
+            for (int i = 0; i < 4; ++i) {
+                const int hh = 4 * g + i;
+                if (hh < G) comb[(wave * D + pv_channel<NCH>(mb, n16)) * kMaxG + hh] = st.o[mb][i];
+            }
     }
-    if (g == 0) {
-        ws.wm[wave][n16] = m_run;
-        ws.wl[wave][n16] = l_run;
-        ws.wo[wave][n16] = off_run;
+    if (g == 0 && n16 < G) {
+        ws.wm[wave][n16] = st.m;
+        ws.wl[wave][n16] = st.l;
+        ws.wo[wave][n16] = st.off;
     }
     __syncthreads();
     for (int i = tid; i < G * D; i += kThreads) {
-        const int h = i / D, c = i - h * D;
+        const int hh = i / D, c = i - hh * D;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ws.wm[w][h]);
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ws.wm[w][hh]);
         float acc = 0.0f, l = 0.0f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
-            const float e = ws.wm[w][h] == -INFINITY ? 0.0f : exp2f(ws.wm[w][h] - M);
-            acc = fmaf(e, comb[(w * D + c) * kMaxG + h] + ws.wo[w][h], acc);
-            l = fmaf(e, ws.wl[w][h], l);
+            const float e = ws.wm[w][hh] == -INFINITY ? 0.0f : exp2f(ws.wm[w][hh] - M);
+            acc = fmaf(e, comb[(w * D + c) * kMaxG + hh] + ws.wo[w][hh], acc);
+            l = fmaf(e, ws.wl[w][hh], l);
         }
-        const size_t qh = qh0 + h;
+        const size_t qh = qh0 + hh;
         partial[(qh * S + split) * D + c] = acc;
         if (c == 0) stats[qh * S + split] = float2{M * 0.69314718055994531f, l};
     }
@@ -227,28 +372,87 @@ struct AstcShared {
     uint32_t key_count[kPathKeys];           // blocks per decode-path class (zero between chunks)
     uint32_t key_base[kPathKeys];            // first sorted position of each class
     uint8_t order[C::kMaxBlocks];            // blocks sorted by decode-path class
+    uint2 q[2 * C::kKSteps][64];             // Q operands (fp16 high, low)
     WaveStats ws;
 };
 
-// The chunk's blocks (one per lane) and their partition-pattern words.
+// The chunk's blocks (one per lane).
 __device__ inline uint4 load_block(const uint4* __restrict__ bseq, uint32_t cols, int row0, int nblk, int tid) {
     return tid < nblk ? bseq[size_t(row0) * cols + tid] : uint4{0, 0, 0, 0};
 }
 
-template <int D, int NCH, int G, bool DUMP>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_ASTC_WAVES))) void astc_attn_kernel(KernelArgs a, const float* __restrict__ q,
-                                                             const uint16_t* __restrict__ k,
-                                                             const uint4* __restrict__ vblk,
-                                                             const uint16_t* __restrict__ vscale,
-                                                             const uint16_t* __restrict__ voffset,
-                                                             const AkvTables* __restrict__ tab,
-                                                             float* __restrict__ partial, float2* __restrict__ stats,
-                                                             uint16_t* __restrict__ dump) {
+// Texels of one 16-token tile straight into the P.V operand: lane (n16, g)
+// decodes tokens t0 + 4g .. + 3 of its texel columns x = n16 + 16 kc. Tokens at
+// or past ntok come out zero. RGBA: channel j of column x feeds row block 4kc + j.
+template <int D, int NCH>
+__device__ __attribute__((always_inline)) inline void tile_texels(const BlockDesc<NCH>* desc, const LdsTables& L, Footprint f, const KernelArgs& a,
+                                   uint32_t cols, const int* bcol, const int* xin, int t0, int ntok, int g,
+                                   uint2 (&tx)[4][Cfg<D, NCH>::kColGroups]) {
     using C = Cfg<D, NCH>;
+    const int tq = t0 + 4 * g;
+    int rk[4], yk[4];
+    {
+        const int tl = min(tq, ntok - 1);   // past the chunk: decode its last token, zeroed below
+        int r = int(fdiv(uint32_t(tl), a.mag_by)), y = tl - r * f.by;
+#pragma unroll
+        for (int tk = 0; tk < 4; ++tk) {
+            rk[tk] = int(__umul24(uint32_t(r), cols));
+            yk[tk] = y;
+            if (tq + tk + 1 < ntok && ++y == f.by) {
+                y = 0;
+                ++r;
+            }
+        }
+    }
+#pragma unroll
+    for (int kc = 0; kc < C::kColGroups; ++kc) {
+        int bk[4], ik[4], xk[4];
+#pragma unroll
+        for (int tk = 0; tk < 4; ++tk) {
+            bk[tk] = rk[tk] + bcol[kc];
+            ik[tk] = int(__umul24(uint32_t(yk[tk]), uint32_t(f.bx))) + xin[kc];
+            xk[tk] = xin[kc];
+        }
+        uint2 tv[4];
+        texels_fp16<NCH, 4>(desc, bk, ik, xk, yk, L, f, tv);
+#pragma unroll
+        for (int tk = 0; tk < 4; ++tk) tx[tk][kc] = tq + tk < ntok ? tv[tk] : uint2{0, 0};
+    }
+}
+
+template <int D, int NCH>
+__device__ inline void texel_operands(const uint2 (&tx)[4][Cfg<D, NCH>::kColGroups], half4* va) {
+    using C = Cfg<D, NCH>;
+#pragma unroll
+    for (int kc = 0; kc < C::kColGroups; ++kc) {
+        if constexpr (NCH == 4) {
+            const uint32_t sel[2] = {0x05040100u, 0x07060302u};
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const uint32_t s = sel[jj & 1];
+                const uint32_t lo = jj < 2 ? __builtin_amdgcn_perm(tx[1][kc].x, tx[0][kc].x, s)
+                                           : __builtin_amdgcn_perm(tx[1][kc].y, tx[0][kc].y, s);
+                const uint32_t hi = jj < 2 ? __builtin_amdgcn_perm(tx[3][kc].x, tx[2][kc].x, s)
+                                           : __builtin_amdgcn_perm(tx[3][kc].y, tx[2][kc].y, s);
+                va[4 * kc + jj] = __builtin_bit_cast(half4, uint2{lo, hi});
+            }
+        } else {
+            va[kc] = __builtin_bit_cast(half4, uint2{tx[0][kc].x | (tx[1][kc].x << 16), tx[2][kc].x | (tx[3][kc].x << 16)});
+        }
+    }
+}
+
+template <int D, int NCH, int G, bool DUMP>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_ASTC_WAVES))) void astc_attn_kernel(
+    KernelArgs a, const float* __restrict__ q, const uint16_t* __restrict__ k, const uint4* __restrict__ vblk,
+    const uint16_t* __restrict__ vscale, const uint16_t* __restrict__ voffset, const AkvTables* __restrict__ tab,
+    float* __restrict__ partial, float2* __restrict__ stats, uint16_t* __restrict__ dump) {
+    using C = Cfg<D, NCH>;
+    constexpr int TPG = Grp<G>::TPG;
     __shared__ AstcShared<D, NCH> sh;
     const AkvAttnParams& p = a.p;
     const Footprint f = a.fp;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int n16 = lane & 15, g = lane >> 4;
     const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
     const int split_begin = split * int(p.tile_tokens);
@@ -267,8 +471,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
     stage_tables(tab, sh.tabs, tid, kThreads);
     if (tid < kPathKeys) sh.key_count[tid] = 0;
 
-    half4 qhi[C::kKSteps], qlo[C::kKSteps];
-    if constexpr (!DUMP) load_q<D, G>(q + (size_t(b) * p.query_heads + size_t(kh) * G) * D, a.qscale, n16, g, qhi, qlo);
+    if constexpr (!DUMP)
+        if (wave == 0) store_q<D, G>(q + (size_t(b) * p.query_heads + size_t(kh) * G) * D, a.qscale, &sh.q[0][0]);
 
     // This lane's texel columns: x = n16 + 16 * kc -> block column and x in block.
     int bcol[C::kColGroups], xin[C::kColGroups];
@@ -279,21 +483,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
         xin[kc] = x - bcol[kc] * f.bx;
     }
 
-    float m_run = -INFINITY, l_run = 0.0f, off_run = 0.0f;
-    floatx4 o[C::kMBlocks];
+    AttnState<D> st;
+    st.m = -INFINITY;
+    st.l = st.off = 0.0f;
 #pragma unroll
-    for (int mb = 0; mb < C::kMBlocks; ++mb) o[mb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int mb = 0; mb < C::kMBlocks; ++mb) st.o[mb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
     for (int c0 = split_begin; c0 < split_end; c0 += CT) {
         const int ntok = min(CT, split_end - c0);
         const int ntiles = (ntok + 15) >> 4;
         const int nblk = chunk_blocks(c0);
-        // 1. Loads, in the order they are needed.
+        // 1. Loads, in the order they are needed: the blocks' partition-pattern
+        // words, this wave's first K group, per-token scale/offset, the next
+        // chunk's blocks.
         const uint4 pw = tid < nblk ? partition_words(raw, tab) : uint4{0, 0, 0, 0};
-        uint4 kcur[C::kRowLoads], knext[C::kRowLoads];
+        uint4 kreg[TPG * C::kRowLoads];
+        const __amdgpu_buffer_rsrc_t krs = seq_rsrc(DUMP ? nullptr : kseq + size_t(c0) * D, DUMP ? 0u : uint32_t(ntok) * D * 2);
         if constexpr (!DUMP) {
-            load_k_tile<D>(kcur, kseq + size_t(c0) * D, 16 * wave, ntok, lane);
-            load_k_tile<D>(knext, kseq + size_t(c0) * D, 16 * (wave + kWaves), ntok, lane);
+#pragma unroll
+            for (int t = 0; t < TPG; ++t)
+                load_k_tile<D>(kreg + t * C::kRowLoads, krs, 16 * (TPG * wave + t), lane);
         }
         // Per-token V scale | offset << 16 for up to two tokens per lane.
         static_assert(C::kMaxTok <= 2 * kThreads, "two scale/offset tokens per lane");
@@ -340,90 +549,50 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
         __syncthreads();
         if (tid < nblk) decode_header<NCH>(sh.tabs, sh.u.h.desc[sh.order[tid]], sh.u.h.cv[tid]);
         __syncthreads();
-        // 3. This wave's tiles (every fourth): the K rows of the tile after
-        // next are requested first, then texels go straight into MFMA
-        // operands, then attention.
-#pragma unroll 1
-        for (int t0 = 16 * wave; t0 < ntok; t0 += 16 * kWaves) {
-            uint4 kafter[C::kRowLoads];   // two tiles ahead
-            if constexpr (!DUMP) load_k_tile<D>(kafter, kseq + size_t(c0) * D, t0 + 32 * kWaves, ntok, lane);
-            const int tq = t0 + 4 * g;   // this lane's 4 tokens: tq .. tq + 3
-            // Tokens past the chunk decode the chunk's last token; zeroed below.
-            int rk[4], yk[4];
-            {
-                const int tl = min(tq, ntok - 1);
-                int r = int(fdiv(uint32_t(tl), a.mag_by)), y = tl - r * by;
-#pragma unroll
-                for (int tk = 0; tk < 4; ++tk) {
-                    rk[tk] = int(__umul24(uint32_t(r), cols));
-                    yk[tk] = y;
-                    if (tq + tk + 1 < ntok && ++y == by) {
-                        y = 0;
-                        ++r;
-                    }
-                }
-            }
-            uint2 tx[4][C::kColGroups];
-#pragma unroll
-            for (int kc = 0; kc < C::kColGroups; ++kc) {
-                int bk[4], ik[4], xk[4];
-#pragma unroll
-                for (int tk = 0; tk < 4; ++tk) {
-                    bk[tk] = rk[tk] + bcol[kc];
-                    ik[tk] = int(__umul24(uint32_t(yk[tk]), uint32_t(f.bx))) + xin[kc];
-                    xk[tk] = xin[kc];
-                }
-                uint2 tv[4];
-                texels_fp16<NCH, 4>(sh.u.h.desc, bk, ik, xk, yk, sh.tabs, f, tv);
-#pragma unroll
-                for (int tk = 0; tk < 4; ++tk) tx[tk][kc] = tq + tk < ntok ? tv[tk] : uint2{0, 0};
-            }
-            if constexpr (DUMP) {
-                uint16_t* dst = dump + (seq_kv * p.tokens + c0) * D;
+        // 3. This wave's groups of TPG consecutive tiles (every fourth group):
+        // S for the whole group, then for each tile its texels straight into
+        // MFMA operands and P.V. The next group's K rows are requested as soon
+        // as S no longer needs the registers.
+        if constexpr (DUMP) {
+            uint16_t* dst = dump + (seq_kv * p.tokens + c0) * D;
+            for (int t0 = 16 * wave; t0 < ntok; t0 += 16 * kWaves) {
+                uint2 tx[4][C::kColGroups];
+                tile_texels<D, NCH>(sh.u.h.desc, sh.tabs, f, a, cols, bcol, xin, t0, ntok, g, tx);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    if (tq + i >= ntok) break;
+                    const int t = t0 + 4 * g + i;
+                    if (t >= ntok) break;
 #pragma unroll
                     for (int kc = 0; kc < C::kColGroups; ++kc) {
                         const int x = n16 + 16 * kc;
-                        if constexpr (NCH == 4) *reinterpret_cast<uint2*>(dst + size_t(tq + i) * D + 4 * x) = tx[i][kc];
-                        else dst[size_t(tq + i) * D + x] = uint16_t(tx[i][kc].x);
+                        if constexpr (NCH == 4) *reinterpret_cast<uint2*>(dst + size_t(t) * D + 4 * x) = tx[i][kc];
+                        else dst[size_t(t) * D + x] = uint16_t(tx[i][kc].x);
                     }
                 }
-                continue;
             }
-            half4 va[C::kMBlocks];
+        } else {
+#pragma unroll 1
+            for (int tb0 = 16 * TPG * wave; tb0 < ntok; tb0 += 16 * TPG * kWaves) {
+                const int ng = min(TPG, (ntok - tb0 + 15) >> 4);
+                attend_group<D, G, true>(
+                    kreg, &sh.q[0][0], ng, tb0, ntok, sh.so, C::kMaxTok, st, [&](int t, half4* va) {
+                        if (t == 0) {   // S is done with this group's K rows
+                            const int nb0 = tb0 + 16 * TPG * kWaves;
 #pragma unroll
-            for (int kc = 0; kc < C::kColGroups; ++kc) {
-                if constexpr (NCH == 4) {
-                    const uint32_t sel[2] = {0x05040100u, 0x07060302u};
-#pragma unroll
-                    for (int jj = 0; jj < 4; ++jj) {
-                        const uint32_t s = sel[jj & 1];
-                        const uint32_t lo = jj < 2 ? __builtin_amdgcn_perm(tx[1][kc].x, tx[0][kc].x, s)
-                                                   : __builtin_amdgcn_perm(tx[1][kc].y, tx[0][kc].y, s);
-                        const uint32_t hi = jj < 2 ? __builtin_amdgcn_perm(tx[3][kc].x, tx[2][kc].x, s)
-                                                   : __builtin_amdgcn_perm(tx[3][kc].y, tx[2][kc].y, s);
-                        va[4 * kc + jj] = __builtin_bit_cast(half4, uint2{lo, hi});
-                    }
-                } else {
-                    va[kc] = __builtin_bit_cast(half4, uint2{tx[0][kc].x | (tx[1][kc].x << 16),
-                                                             tx[2][kc].x | (tx[3][kc].x << 16)});
-                }
-            }
-            const uint4 so4 = *reinterpret_cast<const uint4*>(&sh.so[tq]);
-            attend_tile<D, true>(kcur, qhi, qlo, va, so4, ntok - t0, g, m_run, l_run, off_run, o);
-#pragma unroll
-            for (int L = 0; L < C::kRowLoads; ++L) {
-                kcur[L] = knext[L];
-                knext[L] = kafter[L];
+                            for (int tt = 0; tt < TPG; ++tt)
+                                load_k_tile<D>(kreg + tt * C::kRowLoads, krs, nb0 + 16 * tt, lane);
+                        }
+                        uint2 tx[4][C::kColGroups];
+                        tile_texels<D, NCH>(sh.u.h.desc, sh.tabs, f, a, cols, bcol, xin, tb0 + 16 * t, ntok, g, tx);
+                        texel_operands<D, NCH>(tx, va);
+                    });
             }
         }
         __syncthreads();   // descriptors and so are rewritten by the next chunk
     }
     if constexpr (DUMP) return;
-    combine_waves<D, NCH, G>(sh.u.comb, sh.ws, o, m_run, l_run, off_run, partial, stats,
-                             size_t(b) * p.query_heads + size_t(kh) * G, int(p.splits), split);
+    combine_waves<D, NCH, G>(sh.u.comb, sh.ws, st, partial, stats, size_t(b) * p.query_heads + size_t(kh) * G,
+                             int(p.splits), split);
 }
 
 // --- FP16-K/V control ----------------------------------------------------------
@@ -431,6 +600,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
 template <int D>
 struct Fp16Shared {
     float comb[kWaves * D * kMaxG];
+    uint2 q[2 * D / 16][64];   // Q operands (fp16 high, low)
     WaveStats ws;
 };
 
@@ -439,39 +609,21 @@ struct Fp16Shared {
 // x = n16 + 16k for tokens t0 + 4 * (lane / 16) + i, 8 bytes per token, so 16
 // lanes read 128 contiguous bytes). Tokens at or past ntok read as zero.
 template <int D>
-__device__ inline void load_v_tile(uint2 (&r)[4][D / 64], const uint16_t* __restrict__ seq, int t0, int ntok,
-                                   int lane) {
-    const int n16 = lane & 15, g = lane >> 4;
+__device__ inline void load_v_tile(uint2 (&r)[4][D / 64], __amdgpu_buffer_rsrc_t rs, int t0, int lane) {
+    const uint32_t n16 = uint32_t(lane & 15), g = uint32_t(lane >> 4);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int kc = 0; kc < D / 64; ++kc) {
-            const int t = t0 + 4 * g + i;
-            r[i][kc] = t < ntok ? *reinterpret_cast<const uint2*>(seq + size_t(t) * D + 4 * (n16 + 16 * kc))
-                                : uint2{0, 0};
+            const uint32_t t = uint32_t(t0) + 4 * g + uint32_t(i);
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, 2 * (t * D + 4 * (n16 + 16 * kc)), 0, 0);
+            r[i][kc] = uint2{v[0], v[1]};
         }
 }
 
-template <int D>
-__device__ inline void v_operands(const uint2 (&r)[4][D / 64], half4* va) {
-#pragma unroll
-    for (int kc = 0; kc < D / 64; ++kc) {
-        const uint32_t sel[2] = {0x05040100u, 0x07060302u};
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            const uint32_t s = sel[jj & 1];
-            const uint32_t lo = jj < 2 ? __builtin_amdgcn_perm(r[1][kc].x, r[0][kc].x, s)
-                                       : __builtin_amdgcn_perm(r[1][kc].y, r[0][kc].y, s);
-            const uint32_t hi = jj < 2 ? __builtin_amdgcn_perm(r[3][kc].x, r[2][kc].x, s)
-                                       : __builtin_amdgcn_perm(r[3][kc].y, r[2][kc].y, s);
-            va[4 * kc + jj] = __builtin_bit_cast(half4, uint2{lo, hi});
-        }
-    }
-}
-
-// FP16-K/V control: each wave streams its 16-token tiles of the split (every
-// fourth tile), with the K and V rows of the next two tiles in flight while
-// it computes the current one.
+// FP16-K/V control: each wave streams its groups of TPG tiles of the split
+// (every fourth group); the next group's K rows are requested once S is done
+// with the registers, and each tile's V rows one tile ahead.
 template <int D, int G>
 __global__ __launch_bounds__(kThreads) void fp16_attn_kernel(KernelArgs a, const float* __restrict__ q,
                                                              const uint16_t* __restrict__ k,
@@ -479,48 +631,72 @@ __global__ __launch_bounds__(kThreads) void fp16_attn_kernel(KernelArgs a, const
                                                              float* __restrict__ partial,
                                                              float2* __restrict__ stats) {
     using C = Cfg<D, 4>;
+    constexpr int TPG = Grp<G>::TPG;
     __shared__ Fp16Shared<D> sh;
     const AkvAttnParams& p = a.p;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int n16 = lane & 15, g = lane >> 4;
     const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
     const int split_begin = split * int(p.tile_tokens);
     const int ntok = min(int(p.tile_tokens), int(p.tokens) - split_begin);
     const size_t seq_kv = size_t(b) * p.kv_heads + kh;
-    const uint16_t* kseq = k + (seq_kv * p.tokens + split_begin) * D;
-    const uint16_t* vseq = v + (seq_kv * p.tokens + split_begin) * D;
+    const __amdgpu_buffer_rsrc_t krs = seq_rsrc(k + (seq_kv * p.tokens + split_begin) * D, uint32_t(ntok) * D * 2);
+    const __amdgpu_buffer_rsrc_t vrs = seq_rsrc(v + (seq_kv * p.tokens + split_begin) * D, uint32_t(ntok) * D * 2);
 
-    half4 qhi[C::kKSteps], qlo[C::kKSteps];
-    load_q<D, G>(q + (size_t(b) * p.query_heads + size_t(kh) * G) * D, a.qscale, n16, g, qhi, qlo);
-    float m_run = -INFINITY, l_run = 0.0f, off_run = 0.0f;
-    floatx4 o[C::kMBlocks];
+    if (wave == 0) store_q<D, G>(q + (size_t(b) * p.query_heads + size_t(kh) * G) * D, a.qscale, &sh.q[0][0]);
+    AttnState<D> st;
+    st.m = -INFINITY;
+    st.l = st.off = 0.0f;
 #pragma unroll
-    for (int mb = 0; mb < C::kMBlocks; ++mb) o[mb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int mb = 0; mb < C::kMBlocks; ++mb) st.o[mb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    constexpr int kStride = 16 * kWaves;
-    uint4 k0[C::kRowLoads], k1[C::kRowLoads];
-    uint2 v0[4][D / 64], v1[4][D / 64];
-    int t0 = 16 * wave;
-    load_k_tile<D>(k0, kseq, t0, ntok, lane);
-    load_v_tile<D>(v0, vseq, t0, ntok, lane);
-    load_k_tile<D>(k1, kseq, t0 + kStride, ntok, lane);
-    load_v_tile<D>(v1, vseq, t0 + kStride, ntok, lane);
-    half4 va[C::kMBlocks];
-    for (; t0 < ntok; t0 += 2 * kStride) {
-        v_operands<D>(v0, va);
-        attend_tile<D, false>(k0, qhi, qlo, va, uint4{0, 0, 0, 0}, ntok - t0, g, m_run, l_run, off_run, o);
-        load_k_tile<D>(k0, kseq, t0 + 2 * kStride, ntok, lane);
-        load_v_tile<D>(v0, vseq, t0 + 2 * kStride, ntok, lane);
-        if (t0 + kStride >= ntok) break;
-        v_operands<D>(v1, va);
-        attend_tile<D, false>(k1, qhi, qlo, va, uint4{0, 0, 0, 0}, ntok - t0 - kStride, g, m_run, l_run, off_run,
-                              o);
-        load_k_tile<D>(k1, kseq, t0 + 3 * kStride, ntok, lane);
-        load_v_tile<D>(v1, vseq, t0 + 3 * kStride, ntok, lane);
+    constexpr int kStride = 16 * TPG * kWaves;
+    uint4 kreg[TPG * C::kRowLoads];
+    uint2 vreg[4][D / 64];
+    int tb0 = 16 * TPG * wave;
+#pragma unroll
+    for (int t = 0; t < TPG; ++t) load_k_tile<D>(kreg + t * C::kRowLoads, krs, tb0 + 16 * t, lane);
+    load_v_tile<D>(vreg, vrs, tb0, lane);
+    __syncthreads();   // Q operands
+#pragma unroll 1
+    for (; tb0 < ntok; tb0 += kStride) {
+        const int ng = min(TPG, (ntok - tb0 + 15) >> 4);
+        attend_group<D, G, false>(kreg, &sh.q[0][0], ng, tb0, ntok, nullptr, 4, st,
+                                  [&](int t, half4* va) {
+                                      if (t == 0) {
+#pragma unroll
+                                          for (int tt = 0; tt < TPG; ++tt)
+                                              load_k_tile<D>(kreg + tt * C::kRowLoads, krs, tb0 + kStride + 16 * tt,
+                                                             lane);
+                                      }
+                                      uint2 cur[4][D / 64];
+#pragma unroll
+                                      for (int i = 0; i < 4; ++i)
+#pragma unroll
+                                          for (int kc = 0; kc < D / 64; ++kc) cur[i][kc] = vreg[i][kc];
+                                      // The next tile's V rows (the next group's first tile after the last).
+                                      const int nt = t + 1 < ng ? tb0 + 16 * (t + 1) : tb0 + kStride;
+                                      load_v_tile<D>(vreg, vrs, nt, lane);
+#pragma unroll
+                                      for (int kc = 0; kc < D / 64; ++kc) {
+                                          const uint32_t sel[2] = {0x05040100u, 0x07060302u};
+#pragma unroll
+                                          for (int jj = 0; jj < 4; ++jj) {
+                                              const uint32_t s = sel[jj & 1];
+                                              const uint32_t lo =
+                                                  jj < 2 ? __builtin_amdgcn_perm(cur[1][kc].x, cur[0][kc].x, s)
+                                                         : __builtin_amdgcn_perm(cur[1][kc].y, cur[0][kc].y, s);
+                                              const uint32_t hi =
+                                                  jj < 2 ? __builtin_amdgcn_perm(cur[3][kc].x, cur[2][kc].x, s)
+                                                         : __builtin_amdgcn_perm(cur[3][kc].y, cur[2][kc].y, s);
+                                              va[4 * kc + jj] = __builtin_bit_cast(half4, uint2{lo, hi});
+                                          }
+                                      }
+                                  });
     }
     __syncthreads();
-    combine_waves<D, 4, G>(sh.comb, sh.ws, o, m_run, l_run, off_run, partial, stats,
-                           size_t(b) * p.query_heads + size_t(kh) * G, int(p.splits), split);
+    combine_waves<D, 4, G>(sh.comb, sh.ws, st, partial, stats, size_t(b) * p.query_heads + size_t(kh) * G,
+                           int(p.splits), split);
 }
 
 // --- merge ---------------------------------------------------------------------
