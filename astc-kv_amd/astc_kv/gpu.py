@@ -98,10 +98,10 @@ def default_tile(batch: int, kv_heads: int, tokens: int, chunk: int, block: int 
     * Fewer chunks than CUs: splits of about tokens * batch * kv_heads / CUs
       tokens (at least 16) for parallelism.
     * Up to 8 rounds of resident workgroups (groups_per_cu per CU): the tile
-      (at most one chunk) minimising rounds x (tile + overhead_tokens), i.e.
+      (at most 8 chunks) minimising rounds x (tile + overhead_tokens), i.e.
       the time of the last workgroup to finish when each costs its tokens plus
-      a fixed overhead (a partial last round idles most CUs); the largest tile
-      within 3% of that minimum.
+      a fixed overhead (a partial last round idles most CUs); among tiles
+      within 3% of that minimum, the fewest splits, then the lowest cost.
     * More: several chunks per split (up to 8), which also cuts the
       split-state traffic; the tail is small there."""
     seqs = batch * kv_heads
@@ -111,11 +111,15 @@ def default_tile(batch: int, kv_heads: int, tokens: int, chunk: int, block: int 
         want = max(16, -(-tokens * seqs // cu_count))
         return min(chunk, -(-want // block) * block)
     if total <= 8 * slots:
-        tiles = range(chunk - chunk % block, 0, -block)
+        top = min(8 * chunk, -(-tokens // block) * block)
+        tiles = range(top - top % block, 0, -block)
         cost = {t: -(-seqs * -(-tokens // t) // slots) * (t + overhead_tokens) for t in tiles}
         floor = min(cost.values())
-        # Within 3% of the best, fewer and longer workgroups win (less fixed work).
-        return max(t for t in tiles if cost[t] <= 1.03 * floor)
+        # Within 3% of the best, fewer workgroups win (less fixed work), then
+        # the lower cost (the shortest tile for that many splits).
+        near = [t for t in tiles if cost[t] <= 1.03 * floor]
+        fewest = min(-(-tokens // t) for t in near)
+        return min((cost[t], -t) for t in near if -(-tokens // t) == fewest)[1] * -1
     per_split = max(1, min(8, total // (4 * slots)))
     return per_split * chunk
 

@@ -260,7 +260,7 @@ __device__ __attribute__((always_inline)) inline void weight_fields(const uint32
 
 // Colour integer sequence of this lane's block: range `crange`, `nv` values
 // from bit `start` of the block `blk` (four words in LDS) -> cv[0..].
-__device__ inline void decode_colour_values(const uint32_t* blk, int start, int crange, int nv, const LdsTables& L,
+__device__ __attribute__((always_inline)) inline void decode_colour_values(const uint32_t* blk, int start, int crange, int nv, const LdsTables& L,
                                             uint8_t* cv) {
     const uint4 b4 = *reinterpret_cast<const uint4*>(blk);
     while (true) {
@@ -299,7 +299,7 @@ __device__ inline void decode_colour_values(const uint32_t* blk, int start, int 
 // Weight integer sequence of this lane's block (range `wrange`, `wbits` bits
 // of the bit-reversed block `rev`) -> nb-bit fields in q. Plain ranges are
 // already nb-bit fields.
-__device__ inline void decode_weight_fields(const uint32_t* rev, int wrange, int wbits, const LdsTables& L,
+__device__ __attribute__((always_inline)) inline void decode_weight_fields(const uint32_t* rev, int wrange, int wbits, const LdsTables& L,
                                             uint32_t (&q)[5]) {
     const uint4 r4 = *reinterpret_cast<const uint4*>(rev);
     while (true) {

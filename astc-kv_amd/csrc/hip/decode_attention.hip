@@ -369,6 +369,7 @@ struct AstcShared {
         float comb[kWaves * D * kMaxG];      // final per-wave accumulators
     } u;
     uint32_t so[C::kMaxTok];                 // per-token V scale | offset << 16 (fp16)
+    uint32_t tokrow[C::kMaxTok];             // token_row_entry of each chunk token
     uint32_t key_count[kPathKeys];           // blocks per decode-path class (zero between chunks)
     uint32_t key_base[kPathKeys];            // first sorted position of each class
     uint8_t order[C::kMaxBlocks];            // blocks sorted by decode-path class
@@ -385,39 +386,38 @@ __device__ inline uint4 load_block(const uint4* __restrict__ bseq, uint32_t cols
 // decodes tokens t0 + 4g .. + 3 of its texel columns x = n16 + 16 kc. Tokens at
 // or past ntok come out zero. RGBA: channel j of column x feeds row block 4kc + j.
 template <int D, int NCH>
-__device__ __attribute__((always_inline)) inline void tile_texels(const BlockDesc<NCH>* desc, const LdsTables& L, Footprint f, const KernelArgs& a,
-                                   uint32_t cols, const int* bcol, const int* xin, int t0, int ntok, int g,
-                                   uint2 (&tx)[4][Cfg<D, NCH>::kColGroups]) {
+__device__ __attribute__((always_inline)) inline void tile_texels(const BlockDesc<NCH>* desc, const LdsTables& L,
+                                                                  Footprint f, const uint32_t* tokrow,
+                                                                  const int* bcol, const int* xin, int t0, int g,
+                                                                  uint2 (&tx)[4][Cfg<D, NCH>::kColGroups]) {
     using C = Cfg<D, NCH>;
-    const int tq = t0 + 4 * g;
-    int rk[4], yk[4];
-    {
-        const int tl = min(tq, ntok - 1);   // past the chunk: decode its last token, zeroed below
-        int r = int(fdiv(uint32_t(tl), a.mag_by)), y = tl - r * f.by;
-#pragma unroll
-        for (int tk = 0; tk < 4; ++tk) {
-            rk[tk] = int(__umul24(uint32_t(r), cols));
-            yk[tk] = y;
-            if (tq + tk + 1 < ntok && ++y == f.by) {
-                y = 0;
-                ++r;
-            }
-        }
-    }
+    const uint4 e4 = *reinterpret_cast<const uint4*>(&tokrow[t0 + 4 * g]);
+    const uint32_t e[4] = {e4.x, e4.y, e4.z, e4.w};
 #pragma unroll
     for (int kc = 0; kc < C::kColGroups; ++kc) {
-        int bk[4], ik[4], xk[4];
+        int bk[4], ik[4], xk[4], yk[4];
 #pragma unroll
         for (int tk = 0; tk < 4; ++tk) {
-            bk[tk] = rk[tk] + bcol[kc];
-            ik[tk] = int(__umul24(uint32_t(yk[tk]), uint32_t(f.bx))) + xin[kc];
+            bk[tk] = int(e[tk] >> 16) + bcol[kc];
+            ik[tk] = int(__builtin_amdgcn_ubfe(e[tk], 8, 8)) + xin[kc];
             xk[tk] = xin[kc];
+            yk[tk] = int(e[tk] & 0xFF);
         }
         uint2 tv[4];
         texels_fp16<NCH, 4>(desc, bk, ik, xk, yk, L, f, tv);
 #pragma unroll
-        for (int tk = 0; tk < 4; ++tk) tx[tk][kc] = tq + tk < ntok ? tv[tk] : uint2{0, 0};
+        for (int tk = 0; tk < 4; ++tk) tx[tk][kc] = tv[tk];
     }
+}
+
+// Row table of a chunk: token t -> (first block of its block row) << 16 |
+// (y * bx) << 8 | y, y = t % by. Tokens at or past ntok take the entry of the
+// chunk's last token, so that tile padding decodes real (finite) texels; their
+// probabilities are zero.
+__device__ inline uint32_t token_row_entry(int t, int ntok, uint32_t mag_by, Footprint f, uint32_t cols) {
+    const int tl = min(t, ntok - 1);
+    const int r = int(fdiv(uint32_t(tl), mag_by)), y = tl - r * f.by;
+    return (__umul24(uint32_t(r), cols) << 16) | (uint32_t(y * f.bx) << 8) | uint32_t(y);
 }
 
 template <int D, int NCH>
@@ -449,6 +449,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
     float* __restrict__ partial, float2* __restrict__ stats, uint16_t* __restrict__ dump) {
     using C = Cfg<D, NCH>;
     constexpr int TPG = Grp<G>::TPG;
+    // K tiles of a wave's first group requested before the header stage (their
+    // registers are live through it); the rest right after it.
+    constexpr int kKEarly = TPG < 2 ? TPG : 2;
     __shared__ AstcShared<D, NCH> sh;
     const AkvAttnParams& p = a.p;
     const Footprint f = a.fp;
@@ -501,7 +504,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
         const __amdgpu_buffer_rsrc_t krs = seq_rsrc(DUMP ? nullptr : kseq + size_t(c0) * D, DUMP ? 0u : uint32_t(ntok) * D * 2);
         if constexpr (!DUMP) {
 #pragma unroll
-            for (int t = 0; t < TPG; ++t)
+            for (int t = 0; t < kKEarly; ++t)
                 load_k_tile<D>(kreg + t * C::kRowLoads, krs, 16 * (TPG * wave + t), lane);
         }
         // Per-token V scale | offset << 16 for up to two tokens per lane.
@@ -532,6 +535,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
             for (int i = 0; i < 2; ++i)
                 if (tid + i * kThreads < 16 * ntiles) sh.so[tid + i * kThreads] = so[i];
         }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            if (tid + i * kThreads < C::kMaxTok)
+                sh.tokrow[tid + i * kThreads] = token_row_entry(tid + i * kThreads, ntok, a.mag_by, f, cols);
         __syncthreads();
         if (wave == 0) {   // exclusive scan of the class counts (kPathKeys == 64 lanes)
             const uint32_t c = sh.key_count[lane];
@@ -557,7 +564,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
             uint16_t* dst = dump + (seq_kv * p.tokens + c0) * D;
             for (int t0 = 16 * wave; t0 < ntok; t0 += 16 * kWaves) {
                 uint2 tx[4][C::kColGroups];
-                tile_texels<D, NCH>(sh.u.h.desc, sh.tabs, f, a, cols, bcol, xin, t0, ntok, g, tx);
+                tile_texels<D, NCH>(sh.u.h.desc, sh.tabs, f, sh.tokrow, bcol, xin, t0, g, tx);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int t = t0 + 4 * g + i;
@@ -571,6 +578,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
                 }
             }
         } else {
+#pragma unroll
+            for (int t = kKEarly; t < TPG; ++t)
+                load_k_tile<D>(kreg + t * C::kRowLoads, krs, 16 * (TPG * wave + t), lane);
 #pragma unroll 1
             for (int tb0 = 16 * TPG * wave; tb0 < ntok; tb0 += 16 * TPG * kWaves) {
                 const int ng = min(TPG, (ntok - tb0 + 15) >> 4);
@@ -583,7 +593,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
                                 load_k_tile<D>(kreg + tt * C::kRowLoads, krs, nb0 + 16 * tt, lane);
                         }
                         uint2 tx[4][C::kColGroups];
-                        tile_texels<D, NCH>(sh.u.h.desc, sh.tabs, f, a, cols, bcol, xin, tb0 + 16 * t, ntok, g, tx);
+                        tile_texels<D, NCH>(sh.u.h.desc, sh.tabs, f, sh.tokrow, bcol, xin, tb0 + 16 * t, g, tx);
                         texel_operands<D, NCH>(tx, va);
                     });
             }

@@ -220,13 +220,15 @@ def test_atlas_layout_and_restore(layout, block, d):
 
 def test_default_tiles():
     from astc_kv.gpu import default_tile, fp16_params, tile_for_splits
-    # c3 (48 sequence x kv-head pairs, 265-token chunks): whole chunks, 31 splits
-    # = 1488 workgroups, within two rounds of 3 per CU on 256 CUs.
+    # c3 (48 sequence x kv-head pairs, 265-token chunks): 16 splits = 768
+    # workgroups, one round of 3 per CU on 256 CUs (two rounds of one-chunk
+    # splits cost 2 x (265 + 64) > 515 + 64); the shortest such tile in whole
+    # 5-token block rows.
     t = default_tile(16, 3, 8192, 265, 5)
-    assert t == 265 and 48 * -(-8192 // t) <= 2 * 768
-    # 4x4 (160-token chunks): 52 splits would need 3.25 rounds; about 64 splits fill 4.
+    assert t == 515 and 48 * -(-8192 // t) == 768
+    # 4x4 (160-token chunks): one full round of 16 splits.
     t = default_tile(16, 3, 8192, 160, 4)
-    assert 128 <= t <= 136 and 48 * -(-8192 // t) <= 4 * 768
+    assert t % 4 == 0 and 512 <= t <= 528 and 48 * -(-8192 // t) == 768
     # c4 (64 pairs, 80-token chunks, > 8 rounds): several chunks per split.
     t = default_tile(8, 8, 32768, 80, 4)
     assert t % 80 == 0 and 80 < t <= 8 * 80
