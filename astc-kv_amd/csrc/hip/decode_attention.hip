@@ -471,6 +471,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
 
     auto chunk_blocks = [&](int c0) { return int((min(CT, split_end - c0) + by - 1) / by * cols); };
     uint4 raw = load_block(bseq, cols, split_begin / by, chunk_blocks(split_begin), tid);
+    uint4 pw = tid < chunk_blocks(split_begin) ? partition_words(raw, tab) : uint4{0, 0, 0, 0};
     stage_tables(tab, sh.tabs, tid, kThreads);
     if (tid < kPathKeys) sh.key_count[tid] = 0;
 
@@ -492,14 +493,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
 #pragma unroll
     for (int mb = 0; mb < C::kMBlocks; ++mb) st.o[mb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
+    __syncthreads();   // decode tables and Q operands
     for (int c0 = split_begin; c0 < split_end; c0 += CT) {
         const int ntok = min(CT, split_end - c0);
         const int ntiles = (ntok + 15) >> 4;
         const int nblk = chunk_blocks(c0);
-        // 1. Loads, in the order they are needed: the blocks' partition-pattern
-        // words, this wave's first K group, per-token scale/offset, the next
-        // chunk's blocks.
-        const uint4 pw = tid < nblk ? partition_words(raw, tab) : uint4{0, 0, 0, 0};
+        // 1. Loads (the chunk's blocks and their partition-pattern words were
+        // requested during the previous chunk): the first K tiles of this
+        // wave's first group, per-token scale/offset, the next chunk's blocks.
         uint4 kreg[TPG * C::kRowLoads];
         const __amdgpu_buffer_rsrc_t krs = seq_rsrc(DUMP ? nullptr : kseq + size_t(c0) * D, DUMP ? 0u : uint32_t(ntok) * D * 2);
         if constexpr (!DUMP) {
@@ -519,10 +520,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
         }
         const uint4 raw_now = raw;
         if (c0 + CT < split_end) raw = load_block(bseq, cols, (c0 + CT) / by, chunk_blocks(c0 + CT), tid);
-        // 2. Block headers, with the blocks sorted by decode-path class so that
-        // the lanes of a wave take the same branches. Each block's raw bits and
-        // pattern words wait in its own descriptor slot; the lane that decodes
-        // a block reads them from there and overwrites that slot.
+        // 2. Block headers, with the chunk's blocks sorted by decode-path class
+        // so that the lanes of a wave take the same branches. Each block's raw
+        // bits and pattern words wait in its own descriptor slot; the lane that
+        // decodes a block reads them from there and overwrites that slot.
         int key = 0, rank = 0;
         if (tid < nblk) {
             key = block_path_key(raw_now, sh.tabs);
@@ -555,6 +556,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
         if (tid < nblk) sh.order[sh.key_base[key] + rank] = uint8_t(tid);
         __syncthreads();
         if (tid < nblk) decode_header<NCH>(sh.tabs, sh.u.h.desc[sh.order[tid]], sh.u.h.cv[tid]);
+        // The next chunk's pattern words (its blocks have arrived by now).
+        if (c0 + CT < split_end) pw = tid < chunk_blocks(c0 + CT) ? partition_words(raw, tab) : uint4{0, 0, 0, 0};
         __syncthreads();
         // 3. This wave's groups of TPG consecutive tiles (every fourth group):
         // S for the whole group, then for each tile its texels straight into
