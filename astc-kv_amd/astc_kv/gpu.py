@@ -179,7 +179,9 @@ def make_params(atlas: DeviceAtlas, query_heads: int, tile: int | None = None) -
 
     if tile is None:
         whole = -(-atlas.tokens // atlas.block_y) * atlas.block_y   # one split: the chunk is not clipped
-        tile = default_tile(b, h, atlas.tokens, task_tokens(build(whole)), atlas.block_y)
+        # Resident workgroups per CU: three at head dim 64, two at 128 (registers).
+        tile = default_tile(b, h, atlas.tokens, task_tokens(build(whole)), atlas.block_y,
+                            groups_per_cu=3 if atlas.dim == 64 else 2)
     return build(tile)
 
 

@@ -52,7 +52,9 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 template <int D, int NCH>
 struct Cfg {
-    static constexpr int kMaxBlocks = 160;                       // blocks per chunk (header stage)
+    // Blocks per chunk (header stage, one per lane): at head dim 128 the
+    // kernel runs two workgroups per CU, which leaves room for a full 256.
+    static constexpr int kMaxBlocks = D == 64 ? 160 : 256;
     static constexpr int kMaxTok = D == 64 ? 320 : 128;          // tokens per chunk
     static constexpr int kMaxTiles = kMaxTok / 16;
     static constexpr int kWaveTiles = kMaxTiles / kWaves;        // tiles per wave per chunk
@@ -60,6 +62,7 @@ struct Cfg {
     static constexpr int kKSteps = D / 16;
     static constexpr int kMBlocks = D / 16;
     static constexpr int kColGroups = NCH == 4 ? D / 64 : D / 16; // texel columns per lane
+    static constexpr int kRowBlocksPerGroup = NCH == 4 ? 4 : 1;    // P.V row blocks fed by one column
 };
 
 struct KernelArgs {
@@ -90,9 +93,11 @@ __device__ inline int pv_channel(int mb, int row) {
 // for G <= 4 the softmax runs on 4 head slots instead of the 16 columns of one
 // tile. Q is block-diagonal (row r sees only the K rows of tile t), P likewise
 // for P.V; the MFMA count is the same as one tile at a time.
-template <int G>
+template <int G, int D>
 struct Grp {
-    static constexpr int Gs = G <= 4 ? 4 : 8;   // head slots per tile
+    // Head slots per tile: 4 when G <= 4, except at head dim 128, where the K
+    // rows of four tiles (64 registers) do not fit beside the rest.
+    static constexpr int Gs = (G <= 4 && D <= 64) ? 4 : 8;
     static constexpr int TPG = 16 / Gs;          // tiles per group
 };
 
@@ -103,7 +108,7 @@ struct Grp {
 template <int D, int G>
 __device__ inline void store_q(const float* __restrict__ qrow, float qscale, uint2* qs) {
     const int lane = threadIdx.x & 63, n16 = lane & 15, g = lane >> 4;
-    const int h = n16 % Grp<G>::Gs;
+    const int h = n16 % Grp<G, D>::Gs;
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
         half4 hi, lo;
@@ -183,14 +188,15 @@ struct AttnState {
 };
 
 // One group of up to TPG tiles (ng of them exist) starting at chunk token tb0:
-// kreg[t * D/32 + L] are tile t's K rows; vtile(t, va) produces tile t's V
-// operands (lane (channel, g): tokens 4g..4g+3 of the tile, one half4 per
-// 16-channel block). so: per-token scale | offset << 16 for the chunk (AFFINE).
-template <int D, int G, bool AFFINE, typename VTile>
+// kreg[t * D/32 + L] are tile t's K rows; vtile(t, kc, va) produces tile t's
+// V operands for row blocks MPB*kc .. MPB*kc + MPB-1 (lane (row, g): tokens
+// 4g..4g+3 of the tile), called with kc = 0, 1, ... in order for each tile.
+// so: per-token scale | offset << 16 for the chunk (AFFINE).
+template <int D, int G, bool AFFINE, int MPB, typename VTile>
 __device__ __attribute__((always_inline)) inline void attend_group(const uint4* kreg, const uint2* qs, int ng, int tb0,
                                                                    int ntok, const uint32_t* so, int so_cap,
                                                                    AttnState<D>& st, VTile&& vtile) {
-    constexpr int Gs = Grp<G>::Gs, TPG = Grp<G>::TPG;
+    constexpr int Gs = Grp<G, D>::Gs, TPG = Grp<G, D>::TPG;
     const int lane = threadIdx.x & 63, n16 = lane & 15, g = lane >> 4;
     const int rt = n16 / Gs, h = n16 % Gs;   // this lane's row of S and P: tile, head
     // S^T = K . Q^T per tile, K rows as the A operand and Q as the B operand:
@@ -285,17 +291,22 @@ __device__ __attribute__((always_inline)) inline void attend_group(const uint4* 
             for (int i = 0; i < 4; ++i) st.o[mb][i] *= ar[i];
     }
     const uint2 phib = __builtin_bit_cast(uint2, phi), plob = __builtin_bit_cast(uint2, plo);
-    // O += Pbd . V per tile.
+    // O += Pbd . V per tile, one column group of V operands at a time (MPB
+    // row blocks each), so that only one group's operands are live.
 #pragma unroll
     for (int t = 0; t < TPG; ++t) {
         if (t >= ng) break;
-        half4 va[D / 16];
-        vtile(t, va);
         const half4 ah = masked(phib, tmask[t]), al = masked(plob, tmask[t]);
 #pragma unroll
-        for (int mb = 0; mb < D / 16; ++mb) {
-            st.o[mb] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, va[mb], st.o[mb], 0, 0, 0);
-            st.o[mb] = __builtin_amdgcn_mfma_f32_16x16x16f16(al, va[mb], st.o[mb], 0, 0, 0);
+        for (int kc = 0; kc < D / 16 / MPB; ++kc) {
+            half4 va[MPB];
+            vtile(t, kc, va);
+#pragma unroll
+            for (int j = 0; j < MPB; ++j) {
+                const int mb = kc * MPB + j;
+                st.o[mb] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, va[j], st.o[mb], 0, 0, 0);
+                st.o[mb] = __builtin_amdgcn_mfma_f32_16x16x16f16(al, va[j], st.o[mb], 0, 0, 0);
+            }
         }
     }
 }
@@ -310,7 +321,7 @@ struct WaveStats {
 template <int D, int NCH, int G>
 __device__ inline void combine_waves(float* comb, WaveStats& ws, AttnState<D>& st, float* __restrict__ partial,
                                      float2* __restrict__ stats, size_t qh0, int S, int split) {
-    constexpr int Gs = Grp<G>::Gs;
+    constexpr int Gs = Grp<G, D>::Gs;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n16 = lane & 15, g = lane >> 4;
     // Row partial sums over the tiles of a group and all lanes of a head.
     st.l = lane_allreduce(st.l, Gs, AddOp{});
@@ -385,29 +396,31 @@ __device__ inline uint4 load_block(const uint4* __restrict__ bseq, uint32_t cols
 // Texels of one 16-token tile straight into the P.V operand: lane (n16, g)
 // decodes tokens t0 + 4g .. + 3 of its texel columns x = n16 + 16 kc. Tokens at
 // or past ntok come out zero. RGBA: channel j of column x feeds row block 4kc + j.
-template <int D, int NCH>
-__device__ __attribute__((always_inline)) inline void tile_texels(const BlockDesc<NCH>* desc, const LdsTables& L,
-                                                                  Footprint f, const uint32_t* tokrow,
-                                                                  const int* bcol, const int* xin, int t0, int g,
-                                                                  uint2 (&tx)[4][Cfg<D, NCH>::kColGroups]) {
-    using C = Cfg<D, NCH>;
+// This lane's four tokens of the 16-token tile at t0 (tokens t0 + 4g .. + 3):
+// their token_row_entry values.
+__device__ inline void tile_rows(const uint32_t* tokrow, int t0, int g, uint32_t (&rows)[4]) {
     const uint4 e4 = *reinterpret_cast<const uint4*>(&tokrow[t0 + 4 * g]);
-    const uint32_t e[4] = {e4.x, e4.y, e4.z, e4.w};
+    rows[0] = e4.x;
+    rows[1] = e4.y;
+    rows[2] = e4.z;
+    rows[3] = e4.w;
+}
+
+// Texels of one texel column (block column bcol, x = xin in the block) for
+// the four tokens of `rows`.
+template <int NCH>
+__device__ __attribute__((always_inline)) inline void column_texels(const BlockDesc<NCH>* desc, const LdsTables& L,
+                                                                    Footprint f, const uint32_t (&rows)[4], int bcol,
+                                                                    int xin, uint2 (&tv)[4]) {
+    int bk[4], ik[4], xk[4], yk[4];
 #pragma unroll
-    for (int kc = 0; kc < C::kColGroups; ++kc) {
-        int bk[4], ik[4], xk[4], yk[4];
-#pragma unroll
-        for (int tk = 0; tk < 4; ++tk) {
-            bk[tk] = int(e[tk] >> 16) + bcol[kc];
-            ik[tk] = int(__builtin_amdgcn_ubfe(e[tk], 8, 8)) + xin[kc];
-            xk[tk] = xin[kc];
-            yk[tk] = int(e[tk] & 0xFF);
-        }
-        uint2 tv[4];
-        texels_fp16<NCH, 4>(desc, bk, ik, xk, yk, L, f, tv);
-#pragma unroll
-        for (int tk = 0; tk < 4; ++tk) tx[tk][kc] = tv[tk];
+    for (int tk = 0; tk < 4; ++tk) {
+        bk[tk] = int(rows[tk] >> 16) + bcol;
+        ik[tk] = int(__builtin_amdgcn_ubfe(rows[tk], 8, 8)) + xin;
+        xk[tk] = xin;
+        yk[tk] = int(rows[tk] & 0xFF);
     }
+    texels_fp16<NCH, 4>(desc, bk, ik, xk, yk, L, f, tv);
 }
 
 // Row table of a chunk: token t -> (first block of its block row) << 16 |
@@ -420,35 +433,32 @@ __device__ inline uint32_t token_row_entry(int t, int ntok, uint32_t mag_by, Foo
     return (__umul24(uint32_t(r), cols) << 16) | (uint32_t(y * f.bx) << 8) | uint32_t(y);
 }
 
-template <int D, int NCH>
-__device__ inline void texel_operands(const uint2 (&tx)[4][Cfg<D, NCH>::kColGroups], half4* va) {
-    using C = Cfg<D, NCH>;
+// One column's texels for four tokens -> P.V B operands. RGBA: channel j of
+// the column feeds row block j of the group (lane: tokens 4g .. 4g+3 of
+// channel j); scalar: one row block.
+template <int NCH>
+__device__ inline void texel_operands(const uint2 (&tv)[4], half4* va) {
+    if constexpr (NCH == 4) {
+        const uint32_t sel[2] = {0x05040100u, 0x07060302u};
 #pragma unroll
-    for (int kc = 0; kc < C::kColGroups; ++kc) {
-        if constexpr (NCH == 4) {
-            const uint32_t sel[2] = {0x05040100u, 0x07060302u};
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                const uint32_t s = sel[jj & 1];
-                const uint32_t lo = jj < 2 ? __builtin_amdgcn_perm(tx[1][kc].x, tx[0][kc].x, s)
-                                           : __builtin_amdgcn_perm(tx[1][kc].y, tx[0][kc].y, s);
-                const uint32_t hi = jj < 2 ? __builtin_amdgcn_perm(tx[3][kc].x, tx[2][kc].x, s)
-                                           : __builtin_amdgcn_perm(tx[3][kc].y, tx[2][kc].y, s);
-                va[4 * kc + jj] = __builtin_bit_cast(half4, uint2{lo, hi});
-            }
-        } else {
-            va[kc] = __builtin_bit_cast(half4, uint2{tx[0][kc].x | (tx[1][kc].x << 16), tx[2][kc].x | (tx[3][kc].x << 16)});
+        for (int jj = 0; jj < 4; ++jj) {
+            const uint32_t sl = sel[jj & 1];
+            const uint32_t lo = jj < 2 ? __builtin_amdgcn_perm(tv[1].x, tv[0].x, sl) : __builtin_amdgcn_perm(tv[1].y, tv[0].y, sl);
+            const uint32_t hi = jj < 2 ? __builtin_amdgcn_perm(tv[3].x, tv[2].x, sl) : __builtin_amdgcn_perm(tv[3].y, tv[2].y, sl);
+            va[jj] = __builtin_bit_cast(half4, uint2{lo, hi});
         }
+    } else {
+        va[0] = __builtin_bit_cast(half4, uint2{tv[0].x | (tv[1].x << 16), tv[2].x | (tv[3].x << 16)});
     }
 }
 
 template <int D, int NCH, int G, bool DUMP>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_ASTC_WAVES))) void astc_attn_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 64 ? AKV_ASTC_WAVES : 2))) void astc_attn_kernel(
     KernelArgs a, const float* __restrict__ q, const uint16_t* __restrict__ k, const uint4* __restrict__ vblk,
     const uint16_t* __restrict__ vscale, const uint16_t* __restrict__ voffset, const AkvTables* __restrict__ tab,
     float* __restrict__ partial, float2* __restrict__ stats, uint16_t* __restrict__ dump) {
     using C = Cfg<D, NCH>;
-    constexpr int TPG = Grp<G>::TPG;
+    constexpr int TPG = Grp<G, D>::TPG;
     // K tiles of a wave's first group requested before the header stage (their
     // registers are live through it); the rest right after it.
     constexpr int kKEarly = TPG < 2 ? TPG : 2;
@@ -566,17 +576,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
         if constexpr (DUMP) {
             uint16_t* dst = dump + (seq_kv * p.tokens + c0) * D;
             for (int t0 = 16 * wave; t0 < ntok; t0 += 16 * kWaves) {
-                uint2 tx[4][C::kColGroups];
-                tile_texels<D, NCH>(sh.u.h.desc, sh.tabs, f, sh.tokrow, bcol, xin, t0, g, tx);
+                uint32_t rows[4];
+                tile_rows(sh.tokrow, t0, g, rows);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int t = t0 + 4 * g + i;
-                    if (t >= ntok) break;
+                for (int kc = 0; kc < C::kColGroups; ++kc) {
+                    uint2 tv[4];
+                    column_texels<NCH>(sh.u.h.desc, sh.tabs, f, rows, bcol[kc], xin[kc], tv);
+                    const int x = n16 + 16 * kc;
 #pragma unroll
-                    for (int kc = 0; kc < C::kColGroups; ++kc) {
-                        const int x = n16 + 16 * kc;
-                        if constexpr (NCH == 4) *reinterpret_cast<uint2*>(dst + size_t(t) * D + 4 * x) = tx[i][kc];
-                        else dst[size_t(t) * D + x] = uint16_t(tx[i][kc].x);
+                    for (int i = 0; i < 4; ++i) {
+                        const int t = t0 + 4 * g + i;
+                        if (t >= ntok) break;
+                        if constexpr (NCH == 4) *reinterpret_cast<uint2*>(dst + size_t(t) * D + 4 * x) = tv[i];
+                        else dst[size_t(t) * D + x] = uint16_t(tv[i].x);
                     }
                 }
             }
@@ -587,17 +599,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AKV_AS
 #pragma unroll 1
             for (int tb0 = 16 * TPG * wave; tb0 < ntok; tb0 += 16 * TPG * kWaves) {
                 const int ng = min(TPG, (ntok - tb0 + 15) >> 4);
-                attend_group<D, G, true>(
-                    kreg, &sh.q[0][0], ng, tb0, ntok, sh.so, C::kMaxTok, st, [&](int t, half4* va) {
-                        if (t == 0) {   // S is done with this group's K rows
-                            const int nb0 = tb0 + 16 * TPG * kWaves;
+                uint32_t rows[4];   // token_row_entry of this lane's four tokens of the tile
+                attend_group<D, G, true, C::kRowBlocksPerGroup>(
+                    kreg, &sh.q[0][0], ng, tb0, ntok, sh.so, C::kMaxTok, st, [&](int t, int kc, half4* va) {
+                        if (kc == 0) {
+                            if (t == 0) {   // S is done with this group's K rows
+                                const int nb0 = tb0 + 16 * TPG * kWaves;
 #pragma unroll
-                            for (int tt = 0; tt < TPG; ++tt)
-                                load_k_tile<D>(kreg + tt * C::kRowLoads, krs, nb0 + 16 * tt, lane);
+                                for (int tt = 0; tt < TPG; ++tt)
+                                    load_k_tile<D>(kreg + tt * C::kRowLoads, krs, nb0 + 16 * tt, lane);
+                            }
+                            tile_rows(sh.tokrow, tb0 + 16 * t, g, rows);
                         }
-                        uint2 tx[4][C::kColGroups];
-                        tile_texels<D, NCH>(sh.u.h.desc, sh.tabs, f, sh.tokrow, bcol, xin, tb0 + 16 * t, g, tx);
-                        texel_operands<D, NCH>(tx, va);
+                        uint2 tv[4];
+                        column_texels<NCH>(sh.u.h.desc, sh.tabs, f, rows, bcol[kc], xin[kc], tv);
+                        texel_operands<NCH>(tv, va);
                     });
             }
         }
@@ -644,7 +660,7 @@ __global__ __launch_bounds__(kThreads) void fp16_attn_kernel(KernelArgs a, const
                                                              float* __restrict__ partial,
                                                              float2* __restrict__ stats) {
     using C = Cfg<D, 4>;
-    constexpr int TPG = Grp<G>::TPG;
+    constexpr int TPG = Grp<G, D>::TPG;
     __shared__ Fp16Shared<D> sh;
     const AkvAttnParams& p = a.p;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -665,7 +681,7 @@ __global__ __launch_bounds__(kThreads) void fp16_attn_kernel(KernelArgs a, const
 
     constexpr int kStride = 16 * TPG * kWaves;
     uint4 kreg[TPG * C::kRowLoads];
-    uint2 vreg[4][D / 64];
+    uint2 vreg[4][D / 64], cur[4][D / 64];
     int tb0 = 16 * TPG * wave;
 #pragma unroll
     for (int t = 0; t < TPG; ++t) load_k_tile<D>(kreg + t * C::kRowLoads, krs, tb0 + 16 * t, lane);
@@ -674,38 +690,24 @@ __global__ __launch_bounds__(kThreads) void fp16_attn_kernel(KernelArgs a, const
 #pragma unroll 1
     for (; tb0 < ntok; tb0 += kStride) {
         const int ng = min(TPG, (ntok - tb0 + 15) >> 4);
-        attend_group<D, G, false>(kreg, &sh.q[0][0], ng, tb0, ntok, nullptr, 4, st,
-                                  [&](int t, half4* va) {
-                                      if (t == 0) {
+        attend_group<D, G, false, 4>(kreg, &sh.q[0][0], ng, tb0, ntok, nullptr, 4, st, [&](int t, int kc, half4* va) {
+            if (kc == 0) {
+                if (t == 0) {
 #pragma unroll
-                                          for (int tt = 0; tt < TPG; ++tt)
-                                              load_k_tile<D>(kreg + tt * C::kRowLoads, krs, tb0 + kStride + 16 * tt,
-                                                             lane);
-                                      }
-                                      uint2 cur[4][D / 64];
+                    for (int tt = 0; tt < TPG; ++tt)
+                        load_k_tile<D>(kreg + tt * C::kRowLoads, krs, tb0 + kStride + 16 * tt, lane);
+                }
 #pragma unroll
-                                      for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < 4; ++i)
 #pragma unroll
-                                          for (int kc = 0; kc < D / 64; ++kc) cur[i][kc] = vreg[i][kc];
-                                      // The next tile's V rows (the next group's first tile after the last).
-                                      const int nt = t + 1 < ng ? tb0 + 16 * (t + 1) : tb0 + kStride;
-                                      load_v_tile<D>(vreg, vrs, nt, lane);
-#pragma unroll
-                                      for (int kc = 0; kc < D / 64; ++kc) {
-                                          const uint32_t sel[2] = {0x05040100u, 0x07060302u};
-#pragma unroll
-                                          for (int jj = 0; jj < 4; ++jj) {
-                                              const uint32_t s = sel[jj & 1];
-                                              const uint32_t lo =
-                                                  jj < 2 ? __builtin_amdgcn_perm(cur[1][kc].x, cur[0][kc].x, s)
-                                                         : __builtin_amdgcn_perm(cur[1][kc].y, cur[0][kc].y, s);
-                                              const uint32_t hi =
-                                                  jj < 2 ? __builtin_amdgcn_perm(cur[3][kc].x, cur[2][kc].x, s)
-                                                         : __builtin_amdgcn_perm(cur[3][kc].y, cur[2][kc].y, s);
-                                              va[4 * kc + jj] = __builtin_bit_cast(half4, uint2{lo, hi});
-                                          }
-                                      }
-                                  });
+                    for (int c = 0; c < D / 64; ++c) cur[i][c] = vreg[i][c];
+                // The next tile's V rows (the next group's first tile after the last).
+                const int nt = t + 1 < ng ? tb0 + 16 * (t + 1) : tb0 + kStride;
+                load_v_tile<D>(vreg, vrs, nt, lane);
+            }
+            const uint2 tv[4] = {cur[0][kc], cur[1][kc], cur[2][kc], cur[3][kc]};
+            texel_operands<4>(tv, va);
+        });
     }
     __syncthreads();
     combine_waves<D, 4, G>(sh.comb, sh.ws, st, partial, stats, size_t(b) * p.query_heads + size_t(kh) * G,

@@ -63,9 +63,9 @@ def test_chunk_tokens_follow_the_footprint(hip):
     # Scalar 6x6 D64: 11 block columns -> 14 rows = 84 tokens.
     p = c3(layout=0, block_x=6, block_y=6, atlas_cols=11, atlas_rows=1366, tile_tokens=8196, splits=1)
     assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 84
-    # D128 RGBA 4x4: 8 block columns -> 20 rows = 80 tokens.
+    # D128 RGBA 4x4: 8 block columns, at most 256 blocks -> 32 rows = 128 tokens.
     p = c3(dim=128, block_x=4, block_y=4, atlas_cols=8, atlas_rows=2048, tile_tokens=8192, splits=1)
-    assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 80
+    assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 128
     # FP16 control: whole 320-token chunks (128 for D128).
     assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=8192, splits=1)), 0) == 320
     assert hip.akv_hip_task_tokens(ct.byref(c3(dim=128, tile_tokens=8192, splits=1)), 0) == 128
