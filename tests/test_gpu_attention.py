@@ -98,6 +98,8 @@ def synthetic(rng, b, hq, hkv, t, d, outlier_channels=4, heavy=False):
     ("rgba", (4, 4), 1, 32, 8, 700, 128, True),    # c4 head layout, heavy-tailed K
     ("rgba", (6, 5), 3, 8, 8, 301, 64, False),     # G = 1
     ("rgba", (6, 5), 1, 16, 2, 259, 64, False),    # G = 8
+    ("scalar", (6, 6), 1, 16, 2, 333, 128, False), # scalar head dim 128, G = 8
+    ("rgba", (8, 8), 1, 6, 3, 517, 128, True),     # G = 2, 8x8 footprint
 ])
 def test_synthetic_attention(gpu, layout, block, b, hq, hkv, t, d, heavy):
     from astc_kv.atlas import build_atlas
@@ -135,9 +137,10 @@ def test_split_states_match_oracle(gpu, golden):
     assert u.shape == (1, 3, 391, 64)
 
 
-def test_fp16_control(gpu):
-    rng = np.random.default_rng(5)
-    q, k, v = synthetic(rng, 2, 9, 3, 1111, 64)
+@pytest.mark.parametrize("hq,hkv,d", [(9, 3, 64), (32, 8, 128), (16, 2, 64)])
+def test_fp16_control(gpu, hq, hkv, d):
+    rng = np.random.default_rng(5 + d + hq)
+    q, k, v = synthetic(rng, 2, hq, hkv, 1111, d)
     vh = v.astype(np.float16)
     for tile in (None, 64, 256):
         out = gpu.fp16_attention(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(),
