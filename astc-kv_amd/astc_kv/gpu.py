@@ -43,6 +43,8 @@ def lib():
         P = ct.POINTER(AkvAttnParams)
         vp = ct.c_void_p
         L.akv_hip_decode_attention.argtypes = [P, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        L.akv_hip_decode_attention_fused.argtypes = [P, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        L.akv_hip_fp16_attention_fused.argtypes = [P, vp, vp, vp, vp, vp, vp, vp, vp]
         L.akv_hip_attention_split.argtypes = [P, vp, vp, vp, vp, vp, vp, vp, vp]
         L.akv_hip_attention_merge.argtypes = [P, vp, vp, vp, vp]
         L.akv_hip_fp16_attention.argtypes = [P, vp, vp, vp, vp, vp, vp, vp]
@@ -216,14 +218,47 @@ def attention_merge(params: AkvAttnParams, partial, stats, out=None):
     return out
 
 
+_ARRIVALS: dict = {}
+
+
+def arrivals(device, count: int) -> torch.Tensor:
+    """Zeroed per-(sequence, kv head) counters for the one-launch entry points,
+    cached per device. Every call leaves them zero; calls that may run
+    concurrently (different streams) need their own tensors."""
+    device = torch.device(device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), count)
+    t = _ARRIVALS.get(key)
+    if t is None:
+        t = _ARRIVALS[key] = torch.zeros(count, dtype=torch.int32, device=device)
+    return t
+
+
 def decode_attention(q: torch.Tensor, k: torch.Tensor, atlas: DeviceAtlas, tile: int | None = None,
-                     params: AkvAttnParams | None = None, return_states: bool = False):
+                     params: AkvAttnParams | None = None, return_states: bool = False, partial=None, stats=None,
+                     out=None, fused: bool = True):
     """One decode step: q [B,Hq,D] f32, k [B,Hkv,T,D] f16, V from the ASTC atlas.
-    Returns out [B,Hq,D] f32 (and (partial, stats) if return_states)."""
+    Returns out [B,Hq,D] f32 (and (partial, stats) if return_states). fused:
+    one launch (the last split workgroup of a kv head merges); otherwise the
+    split and merge passes."""
     if params is None:
         params = make_params(atlas, q.shape[1], tile)
-    partial, stats = attention_split(q, k, atlas, params)
-    out = attention_merge(params, partial, stats)
+    if not fused:
+        partial, stats = attention_split(q, k, atlas, params, partial, stats)
+        out = attention_merge(params, partial, stats, out)
+        return (out, partial, stats) if return_states else out
+    b, hq, d = q.shape
+    _check_qk(q, k, atlas.batch, atlas.kv_heads, atlas.tokens, atlas.dim)
+    s = params.splits
+    if partial is None:
+        partial = torch.empty((b, hq, s, d), dtype=torch.float32, device=q.device)
+    if stats is None:
+        stats = torch.empty((b, hq, s, 2), dtype=torch.float32, device=q.device)
+    if out is None:
+        out = torch.empty((b, hq, d), dtype=torch.float32, device=q.device)
+    _check(lib().akv_hip_decode_attention_fused(ct.byref(params), _ptr(q), _ptr(k), _ptr(atlas.blocks),
+                                                _ptr(atlas.scale), _ptr(atlas.offset), _ptr(partial), _ptr(stats),
+                                                _ptr(out), _ptr(arrivals(q.device, b * atlas.kv_heads)),
+                                                _stream(q.device)))
     return (out, partial, stats) if return_states else out
 
 
@@ -240,8 +275,9 @@ def fp16_params(batch, kv_heads, query_heads, tokens, dim, tile=None, cu_count: 
 
 
 def fp16_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tile: int | None = None,
-                   params: AkvAttnParams | None = None, partial=None, stats=None, out=None):
-    """FP16-K/V control: same schedule, V read as restored fp16 [B,Hkv,T,D]."""
+                   params: AkvAttnParams | None = None, partial=None, stats=None, out=None, fused: bool = True):
+    """FP16-K/V control: same schedule, V read as restored fp16 [B,Hkv,T,D];
+    fused as in decode_attention."""
     b, hkv, t, d = k.shape
     _check_qk(q, k, b, hkv, t, d)
     _need(v, torch.float16, "v", (b, hkv, t, d))
@@ -254,8 +290,9 @@ def fp16_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tile: int 
         stats = torch.empty((b, q.shape[1], s, 2), dtype=torch.float32, device=q.device)
     if out is None:
         out = torch.empty((b, q.shape[1], d), dtype=torch.float32, device=q.device)
-    _check(lib().akv_hip_fp16_attention(ct.byref(params), _ptr(q), _ptr(k), _ptr(v), _ptr(partial), _ptr(stats),
-                                        _ptr(out), _stream(q.device)))
+    arr = arrivals(q.device, b * hkv) if fused else None
+    _check(lib().akv_hip_fp16_attention_fused(ct.byref(params), _ptr(q), _ptr(k), _ptr(v), _ptr(partial),
+                                              _ptr(stats), _ptr(out), _ptr(arr), _stream(q.device)))
     return out
 
 

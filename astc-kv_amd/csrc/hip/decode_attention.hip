@@ -313,7 +313,86 @@ __device__ __attribute__((always_inline)) inline void attend_group(const uint4* 
 
 struct WaveStats {
     float wm[kWaves][kMaxG], wl[kWaves][kMaxG], wo[kWaves][kMaxG];
+    int last;   // this workgroup is the last split of its (sequence, kv head) to finish
 };
+
+// Merge done by the split kernel itself: after writing its split state, a
+// workgroup counts itself in `arrival` (one counter per (sequence, kv head));
+// the last of the S workgroups merges the G query heads' S states into `out`
+// exactly as merge_kernel does, and leaves the counter at zero for the next
+// launch. No workgroup waits for another. The states are written and read
+// with agent-scope atomic accesses (write-through stores, coherent loads), so
+// publishing them needs no L2 write-back or invalidation: the stores of every
+// wave complete (s_waitcnt 0) before the barrier, and the counter increment
+// comes after it.
+template <int D, int G>
+__device__ inline void merge_if_last(uint32_t* arrival, const float* partial, const float2* stats,
+                                     float* __restrict__ out, size_t qh0, int S, WaveStats& ws, float* lds,
+                                     int lds_floats) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        ws.last = __hip_atomic_fetch_add(arrival, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == uint32_t(S - 1);
+    __syncthreads();
+    if (!ws.last) return;
+    const int tid = threadIdx.x;
+    auto load = [](const float* x) { return __hip_atomic_load(x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    auto load2 = [](const float2* x) {
+        return __builtin_bit_cast(float2, __hip_atomic_load(reinterpret_cast<const uint64_t*>(x), __ATOMIC_RELAXED,
+                                                            __HIP_MEMORY_SCOPE_AGENT));
+    };
+    if (2 * G * S + 2 * G <= lds_floats) {
+        // Stats of the G heads' S splits into LDS (one load each, all in flight),
+        // then per head the maximum, the split weights e^(m_s - M) and the sum l.
+        float2* w = reinterpret_cast<float2*>(lds);   // [G][S]: (m, l) -> (weight, -)
+        float* linv = lds + 2 * G * S;                // [G]: 1 / sum of weighted l
+        for (int i = tid; i < G * S; i += kThreads) w[i] = load2(&stats[qh0 * S + i]);
+        __syncthreads();
+        if (tid < G) {
+            float M = -INFINITY, l = 0.0f;
+            for (int sp = 0; sp < S; ++sp) M = fmaxf(M, w[tid * S + sp].x);
+            for (int sp = 0; sp < S; ++sp) {
+                const float2 ms = w[tid * S + sp];
+                const float e = ms.x == -INFINITY ? 0.0f : expf(ms.x - M);
+                w[tid * S + sp].x = e;
+                l = fmaf(ms.y, e, l);
+            }
+            linv[tid] = 1.0f / l;
+        }
+        __syncthreads();
+        for (int i = tid; i < G * D; i += kThreads) {
+            const int hh = i / D, c = i - hh * D;
+            const float* src = partial + (qh0 + hh) * size_t(S) * D + c;
+            float acc = 0.0f;
+            int sp = 0;
+            for (; sp + 8 <= S; sp += 8) {
+                float x[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x[j] = load(src + size_t(sp + j) * D);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc = fmaf(x[j], w[hh * S + sp + j].x, acc);
+            }
+            for (; sp < S; ++sp) acc = fmaf(load(src + size_t(sp) * D), w[hh * S + sp].x, acc);
+            out[(qh0 + hh) * D + c] = acc * linv[hh];
+        }
+    } else {
+        for (int i = tid; i < G * D; i += kThreads) {
+            const int hh = i / D, c = i - hh * D;
+            const size_t qh = qh0 + hh;
+            float M = -INFINITY;
+            for (int sp = 0; sp < S; ++sp) M = fmaxf(M, load2(&stats[qh * S + sp]).x);
+            float acc = 0.0f, l = 0.0f;
+            for (int sp = 0; sp < S; ++sp) {
+                const float2 ms = load2(&stats[qh * S + sp]);
+                const float e = ms.x == -INFINITY ? 0.0f : expf(ms.x - M);
+                l = fmaf(ms.y, e, l);
+                acc = fmaf(load(&partial[(qh * S + sp) * D + c]), e, acc);
+            }
+            out[qh * D + c] = acc / l;
+        }
+    }
+    if (tid == 0) __hip_atomic_store(arrival, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Combine: each wave sums its rows over the group's tiles and over lanes, then
 // the four waves' states merge into this split's (partial, stats). comb:
@@ -361,8 +440,14 @@ __device__ inline void combine_waves(float* comb, WaveStats& ws, AttnState<D>& s
             l = fmaf(e, ws.wl[w][hh], l);
         }
         const size_t qh = qh0 + hh;
-        partial[(qh * S + split) * D + c] = acc;
-        if (c == 0) stats[qh * S + split] = float2{M * 0.69314718055994531f, l};
+        // Agent-scope stores (written through to the device coherence point),
+        // so that the workgroup merging the splits can read them from any XCD.
+        __hip_atomic_store(&partial[(qh * S + split) * D + c], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (c == 0) {
+            const float2 ml{M * 0.69314718055994531f, l};
+            __hip_atomic_store(reinterpret_cast<uint64_t*>(&stats[qh * S + split]), __builtin_bit_cast(uint64_t, ml),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 
@@ -456,7 +541,7 @@ template <int D, int NCH, int G, bool DUMP>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 64 ? AKV_ASTC_WAVES : 2))) void astc_attn_kernel(
     KernelArgs a, const float* __restrict__ q, const uint16_t* __restrict__ k, const uint4* __restrict__ vblk,
     const uint16_t* __restrict__ vscale, const uint16_t* __restrict__ voffset, const AkvTables* __restrict__ tab,
-    float* __restrict__ partial, float2* __restrict__ stats, uint16_t* __restrict__ dump) {
+    float* partial, float2* stats, uint16_t* __restrict__ dump, float* __restrict__ out, uint32_t* arrivals) {
     using C = Cfg<D, NCH>;
     constexpr int TPG = Grp<G, D>::TPG;
     // K tiles of a wave's first group requested before the header stage (their
@@ -620,8 +705,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
         __syncthreads();   // descriptors and so are rewritten by the next chunk
     }
     if constexpr (DUMP) return;
-    combine_waves<D, NCH, G>(sh.u.comb, sh.ws, st, partial, stats, size_t(b) * p.query_heads + size_t(kh) * G,
-                             int(p.splits), split);
+    const size_t qh0 = size_t(b) * p.query_heads + size_t(kh) * G;
+    combine_waves<D, NCH, G>(sh.u.comb, sh.ws, st, partial, stats, qh0, int(p.splits), split);
+    if (arrivals)
+        merge_if_last<D, G>(arrivals + seq_kv, partial, stats, out, qh0, int(p.splits), sh.ws, sh.u.comb,
+                            kWaves * D * kMaxG);
 }
 
 // --- FP16-K/V control ----------------------------------------------------------
@@ -657,8 +745,8 @@ template <int D, int G>
 __global__ __launch_bounds__(kThreads) void fp16_attn_kernel(KernelArgs a, const float* __restrict__ q,
                                                              const uint16_t* __restrict__ k,
                                                              const uint16_t* __restrict__ v,
-                                                             float* __restrict__ partial,
-                                                             float2* __restrict__ stats) {
+                                                             float* partial, float2* stats,
+                                                             float* __restrict__ out, uint32_t* arrivals) {
     using C = Cfg<D, 4>;
     constexpr int TPG = Grp<G, D>::TPG;
     __shared__ Fp16Shared<D> sh;
@@ -710,8 +798,11 @@ __global__ __launch_bounds__(kThreads) void fp16_attn_kernel(KernelArgs a, const
         });
     }
     __syncthreads();
-    combine_waves<D, 4, G>(sh.comb, sh.ws, st, partial, stats, size_t(b) * p.query_heads + size_t(kh) * G,
-                           int(p.splits), split);
+    const size_t qh0 = size_t(b) * p.query_heads + size_t(kh) * G;
+    combine_waves<D, 4, G>(sh.comb, sh.ws, st, partial, stats, qh0, int(p.splits), split);
+    if (arrivals)
+        merge_if_last<D, G>(arrivals + seq_kv, partial, stats, out, qh0, int(p.splits), sh.ws, sh.comb,
+                            kWaves * D * kMaxG);
 }
 
 // --- merge ---------------------------------------------------------------------
@@ -901,6 +992,8 @@ struct Ptrs {
     float* partial;
     float* stats;
     uint16_t* dump;
+    float* out = nullptr;             // with arrivals: the merged output
+    uint32_t* arrivals = nullptr;     // non-null: merge in the split kernel
 };
 
 template <int D, int NCH, bool DUMP>
@@ -909,14 +1002,15 @@ hipError_t launch_astc_g(const KernelArgs& a, uint32_t G, const Ptrs& x, hipStre
     auto* s2 = reinterpret_cast<float2*>(x.stats);
     if constexpr (DUMP) {
         astc_attn_kernel<D, NCH, 1, true><<<grid, kThreads, 0, st>>>(a, x.q, x.k, x.vblk, x.vs, x.vo, x.tab, x.partial,
-                                                                      s2, x.dump);
+                                                                      s2, x.dump, nullptr, nullptr);
         return hipGetLastError();
     }
     switch (G) {
 #define AKV_CASE(GG)                                                                                       \
     case GG:                                                                                               \
         astc_attn_kernel<D, NCH, GG, DUMP><<<grid, kThreads, 0, st>>>(a, x.q, x.k, x.vblk, x.vs, x.vo, x.tab, \
-                                                                       x.partial, s2, x.dump);            \
+                                                                       x.partial, s2, x.dump, x.out,      \
+                                                                       x.arrivals);                       \
         break;
         AKV_CASE(1)
         AKV_CASE(2)
@@ -944,7 +1038,8 @@ hipError_t launch_fp16_g(const KernelArgs& a, uint32_t G, const Ptrs& x, hipStre
     switch (G) {
 #define AKV_CASE(GG)                                                                                   \
     case GG:                                                                                           \
-        fp16_attn_kernel<D, GG><<<grid, kThreads, 0, st>>>(a, x.q, x.k, x.vh, x.partial, s2);         \
+        fp16_attn_kernel<D, GG><<<grid, kThreads, 0, st>>>(a, x.q, x.k, x.vh, x.partial, s2, x.out,   \
+                                                           x.arrivals);                                 \
         break;
         AKV_CASE(1)
         AKV_CASE(2)
@@ -969,7 +1064,8 @@ hipError_t launch_merge(const AkvAttnParams* p, const float* partial, const floa
 }
 
 int run_astc(const AkvAttnParams* p, const float* q, const uint16_t* k, const void* v_blocks, const uint16_t* v_scale,
-             const uint16_t* v_offset, float* partial, float* stats, float* out, bool with_merge, void* stream) {
+             const uint16_t* v_offset, float* partial, float* stats, float* out, bool with_merge, uint32_t* arrivals,
+             void* stream) {
     uint32_t G = 0;
     if (int rc = check_common(p, &G)) return rc;
     if (int rc = check_astc(p)) return rc;
@@ -980,9 +1076,13 @@ int run_astc(const AkvAttnParams* p, const float* q, const uint16_t* k, const vo
     KernelArgs a;
     if (int rc = make_args(p, true, &a)) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const Ptrs x{q, k, static_cast<const uint4*>(v_blocks), nullptr, v_scale, v_offset, tab, partial, stats, nullptr};
+    Ptrs x{q, k, static_cast<const uint4*>(v_blocks), nullptr, v_scale, v_offset, tab, partial, stats, nullptr};
+    if (with_merge && arrivals) {
+        x.out = out;
+        x.arrivals = arrivals;
+    }
     hipError_t e = launch_astc<false>(a, G, x, st);
-    if (e == hipSuccess && with_merge) e = launch_merge(p, partial, stats, out, st);
+    if (e == hipSuccess && with_merge && !arrivals) e = launch_merge(p, partial, stats, out, st);
     return as_int(e);
 }
 
@@ -996,7 +1096,7 @@ extern "C" {
 int akv_hip_attention_split(const AkvAttnParams* p, const float* q, const uint16_t* k, const void* v_blocks,
                             const uint16_t* v_scale, const uint16_t* v_offset, float* partial, float* stats,
                             void* stream) {
-    return run_astc(p, q, k, v_blocks, v_scale, v_offset, partial, stats, nullptr, false, stream);
+    return run_astc(p, q, k, v_blocks, v_scale, v_offset, partial, stats, nullptr, false, nullptr, stream);
 }
 
 int akv_hip_attention_merge(const AkvAttnParams* p, const float* partial, const float* stats, float* out,
@@ -1010,21 +1110,35 @@ int akv_hip_attention_merge(const AkvAttnParams* p, const float* partial, const 
 int akv_hip_decode_attention(const AkvAttnParams* p, const float* q, const uint16_t* k, const void* v_blocks,
                              const uint16_t* v_scale, const uint16_t* v_offset, float* partial, float* stats,
                              float* out, void* stream) {
-    return run_astc(p, q, k, v_blocks, v_scale, v_offset, partial, stats, out, true, stream);
+    return run_astc(p, q, k, v_blocks, v_scale, v_offset, partial, stats, out, true, nullptr, stream);
 }
 
-int akv_hip_fp16_attention(const AkvAttnParams* p, const float* q, const uint16_t* k, const uint16_t* v,
-                           float* partial, float* stats, float* out, void* stream) {
+int akv_hip_decode_attention_fused(const AkvAttnParams* p, const float* q, const uint16_t* k, const void* v_blocks,
+                                   const uint16_t* v_scale, const uint16_t* v_offset, float* partial, float* stats,
+                                   float* out, uint32_t* arrivals, void* stream) {
+    if (!arrivals) return AKV_HIP_ERR_NULL;
+    return run_astc(p, q, k, v_blocks, v_scale, v_offset, partial, stats, out, true, arrivals, stream);
+}
+
+int akv_hip_fp16_attention_fused(const AkvAttnParams* p, const float* q, const uint16_t* k, const uint16_t* v,
+                                 float* partial, float* stats, float* out, uint32_t* arrivals, void* stream) {
     uint32_t G = 0;
     if (int rc = check_common(p, &G)) return rc;
     if (!q || !k || !v || !partial || !stats || !out) return AKV_HIP_ERR_NULL;
     KernelArgs a;
     if (int rc = make_args(p, false, &a)) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const Ptrs x{q, k, nullptr, v, nullptr, nullptr, nullptr, partial, stats, nullptr};
+    Ptrs x{q, k, nullptr, v, nullptr, nullptr, nullptr, partial, stats, nullptr};
+    x.out = out;
+    x.arrivals = arrivals;
     hipError_t e = p->dim == 64 ? launch_fp16_g<64>(a, G, x, st) : launch_fp16_g<128>(a, G, x, st);
-    if (e == hipSuccess) e = launch_merge(p, partial, stats, out, st);
+    if (e == hipSuccess && !arrivals) e = launch_merge(p, partial, stats, out, st);
     return as_int(e);
+}
+
+int akv_hip_fp16_attention(const AkvAttnParams* p, const float* q, const uint16_t* k, const uint16_t* v,
+                           float* partial, float* stats, float* out, void* stream) {
+    return akv_hip_fp16_attention_fused(p, q, k, v, partial, stats, out, nullptr, stream);
 }
 
 int akv_hip_decode_values(const AkvAttnParams* p, const void* v_blocks, uint16_t* u, void* stream) {

@@ -286,23 +286,18 @@ def main(argv=None):
         torch.cuda.synchronize()
         del src, dst
 
+    # One launch per step: the split kernel with the merge done by the last
+    # split workgroup of each (sequence, kv head).
     def step(i):
         kk, dd = pool[i % pool_n]
-        gpu.attention_split(qt, kk, dd, params, partial, stats)
-        gpu.attention_merge(params, partial, stats, out)
-
-    def split_only(i):
-        kk, dd = pool[i % pool_n]
-        gpu.attention_split(qt, kk, dd, params, partial, stats)
+        gpu.decode_attention(qt, kk, dd, params=params, partial=partial, stats=stats, out=out)
 
     torch.cuda.synchronize()
     log(f"timing {a.steps} steps (tile {params.tile_tokens}, {s} splits, pool of {pool_n} KV sets)")
     ms_step, mode = time_graph(torch, step, a.steps, a.warmup, not a.no_graph)
-    ms_split, _ = time_graph(torch, split_only, a.steps, a.warmup, not a.no_graph)
 
     def resident(i):
-        gpu.attention_split(qt, kt, dev, params, partial, stats)
-        gpu.attention_merge(params, partial, stats, out)
+        gpu.decode_attention(qt, kt, dev, params=params, partial=partial, stats=stats, out=out)
 
     ms_resident, _ = time_graph(torch, resident, a.steps, a.warmup, not a.no_graph)
 
@@ -365,7 +360,7 @@ def main(argv=None):
                "us_per_step": round(sec * 1e6, 1), "us_per_step_1core": round(sec1 * 1e6, 1),
                "astc_decode_us_1core": round(decode_s * 1e6, 1)}
 
-    achieved = nbytes["split"] / (ms_split * 1e-3) / 1e9
+    achieved = nbytes["step"] / (ms_step * 1e-3) / 1e9
     value = nbytes["step"] / (ms_step * 1e-3) / 1e9
     traffic = read_traffic(a.traffic, workload_name(a))
     line = {
@@ -392,8 +387,8 @@ def main(argv=None):
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic["bytes"] if traffic else None,
                      "traffic_source": traffic["source"] if traffic else None,
-                     "kernel": "astc_attn_kernel (split, ASTC V)", "bytes_per_launch": nbytes["split"],
-                     "us_per_launch": round(ms_split * 1e3, 3)},
+                     "kernel": "astc_attn_kernel (split + in-kernel merge, ASTC V)",
+                     "bytes_per_launch": nbytes["step"], "us_per_launch": round(ms_step * 1e3, 3)},
         "cpu_baseline": cpu,
         "resident_single_set": {"us_per_step": round(ms_resident * 1e3, 3),
                                 "GB/s": round(nbytes["step"] / (ms_resident * 1e-3) / 1e9, 2)},

@@ -9,6 +9,8 @@
  * dispatches:
  *   akv_hip_decode_attention  split (attention_split_gqa3, :568-674) + merge
  *                             (attention_merge, :229-253), ASTC V
+ *   akv_hip_decode_attention_fused  the same in one launch (merge by the
+ *                             last split workgroup; caller-owned counters)
  *   akv_hip_attention_split   the split pass alone
  *   akv_hip_attention_merge   the merge pass alone
  *   akv_hip_fp16_attention    the FP16 K/V control (fp16_buffer variant,
@@ -83,6 +85,17 @@ int akv_hip_decode_attention(const AkvAttnParams* p, const float* q, const uint1
                              const uint16_t* v_scale, const uint16_t* v_offset, float* partial, float* stats,
                              float* out, void* stream);
 
+/* As akv_hip_decode_attention in one launch: the last split workgroup of each
+   (sequence, kv head) to finish merges that kv head's query heads (no second
+   pass; results equal the merge pass up to summation order). `arrivals`:
+   caller workspace of batch * kv_heads uint32 counters, zero before the first
+   call; every call leaves them zero. Concurrent calls must not share it. No
+   counterpart in the reference, whose merge is always a second dispatch
+   (probe_gqa_v10.mm:648-681). */
+int akv_hip_decode_attention_fused(const AkvAttnParams* p, const float* q, const uint16_t* k, const void* v_blocks,
+                                   const uint16_t* v_scale, const uint16_t* v_offset, float* partial, float* stats,
+                                   float* out, uint32_t* arrivals, void* stream);
+
 int akv_hip_attention_split(const AkvAttnParams* p, const float* q, const uint16_t* k, const void* v_blocks,
                             const uint16_t* v_scale, const uint16_t* v_offset, float* partial, float* stats,
                             void* stream);
@@ -94,6 +107,11 @@ int akv_hip_attention_merge(const AkvAttnParams* p, const float* partial, const 
    batch, tokens, query_heads, kv_heads, dim, tile_tokens and splits only. */
 int akv_hip_fp16_attention(const AkvAttnParams* p, const float* q, const uint16_t* k, const uint16_t* v,
                            float* partial, float* stats, float* out, void* stream);
+
+/* The FP16 control with the merge in the split launch, as
+   akv_hip_decode_attention_fused (arrivals may be NULL: two launches). */
+int akv_hip_fp16_attention_fused(const AkvAttnParams* p, const float* q, const uint16_t* k, const uint16_t* v,
+                                 float* partial, float* stats, float* out, uint32_t* arrivals, void* stream);
 
 /* Normalised V exactly as the attention kernel decodes it: FP16 bit patterns
    [batch][kv_heads][tokens][dim]. */

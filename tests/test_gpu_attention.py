@@ -171,3 +171,24 @@ def test_full_size_c3_properties(gpu):
     from astc_kv.atlas import Atlas
     small = Atlas(atlas.blocks[sub], atlas.scale[sub], atlas.offset[sub], t, 64, "rgba", 6, 5, 120)
     check(out[sub], q[sub], k[sub], oracle_v(small))
+
+
+def test_fused_merge_matches_two_launches(gpu):
+    """One-launch step (merge by the last split workgroup) against split + merge
+    launches; repeated calls reuse the arrival counters (left at zero)."""
+    from astc_kv.atlas import build_atlas
+    from astc_kv.gpu import DeviceAtlas
+    rng = np.random.default_rng(77)
+    q, k, v = synthetic(rng, 3, 9, 3, 1200, 64)
+    dev = DeviceAtlas.from_host(build_atlas(v, "rgba", (6, 5), page_tokens=120, quality=30))
+    qt, kt = torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda()
+    for tile in (None, 60, 265):
+        two = gpu.decode_attention(qt, kt, dev, tile, fused=False).cpu().numpy()
+        outs = [gpu.decode_attention(qt, kt, dev, tile).cpu().numpy() for _ in range(3)]
+        for o in outs:
+            assert np.array_equal(o, outs[0])
+            np.testing.assert_allclose(o, two, rtol=2e-6, atol=1e-7)
+    assert int(gpu.arrivals(qt.device, 3 * 3).abs().sum()) == 0
+    vh = torch.from_numpy(v.astype(np.float16)).cuda()
+    np.testing.assert_allclose(gpu.fp16_attention(qt, kt, vh, 128).cpu().numpy(),
+                               gpu.fp16_attention(qt, kt, vh, 128, fused=False).cpu().numpy(), rtol=2e-6, atol=1e-7)
