@@ -31,6 +31,15 @@ class AkvAttnParams(ct.Structure):
         "layout", "block_x", "block_y", "atlas_rows", "atlas_cols")]
 
 
+class AkvPagedParams(ct.Structure):
+    _fields_ = [(name, ct.c_uint32) for name in (
+        "batch", "max_tokens", "query_heads", "kv_heads", "dim", "page_tokens", "max_pages", "num_pages",
+        "tile_tokens", "splits", "layout", "block_x", "block_y", "atlas_cols", "k_format")]
+
+
+K_FORMATS = {"fp16": 0, "u4g32": 1}
+
+
 def lib():
     """Load the HIP extension; raises if it is absent or no GPU is visible."""
     global _LIB
@@ -50,6 +59,10 @@ def lib():
         L.akv_hip_fp16_attention.argtypes = [P, vp, vp, vp, vp, vp, vp, vp]
         L.akv_hip_decode_values.argtypes = [P, vp, vp, vp]
         L.akv_hip_decode_blocks.argtypes = [vp, ct.c_size_t, ct.c_uint, ct.c_uint, vp, vp]
+        PP = ct.POINTER(AkvPagedParams)
+        L.akv_hip_paged_decode_attention.argtypes = [PP] + [vp] * 14
+        L.akv_hip_paged_task_tokens.argtypes = [PP]
+        L.akv_hip_paged_task_tokens.restype = ct.c_int
         L.akv_hip_task_tokens.argtypes = [P, ct.c_int]
         L.akv_hip_task_tokens.restype = ct.c_int
         L.akv_hip_error_string.argtypes = [ct.c_int]
@@ -312,3 +325,97 @@ def decode_blocks(blocks: torch.Tensor, block_x: int, block_y: int) -> torch.Ten
     out = torch.empty((n, block_y, block_x, 4), dtype=torch.float16, device=blocks.device)
     _check(lib().akv_hip_decode_blocks(_ptr(blocks), n, block_x, block_y, _ptr(out), _stream(blocks.device)))
     return out
+
+
+# --- paged, ragged batches -----------------------------------------------------
+
+@dataclass
+class DevicePagedKV:
+    """A PagedKV (astc_kv.paged) resident in GPU memory."""
+    k_pages: torch.Tensor
+    k_meta: torch.Tensor | None
+    v_blocks: torch.Tensor
+    v_scale: torch.Tensor
+    v_offset: torch.Tensor
+    block_table: torch.Tensor
+    seq_lens: torch.Tensor
+    v_tail: torch.Tensor | None
+    lens: list
+    dim: int
+    layout: str
+    block_x: int
+    block_y: int
+    page_tokens: int
+    k_format: str
+
+    @classmethod
+    def from_host(cls, pk, device="cuda") -> "DevicePagedKV":
+        def dev(a):
+            return None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(device)
+        return cls(dev(pk.k_pages), dev(pk.k_meta), dev(pk.v_blocks), dev(pk.v_scale), dev(pk.v_offset),
+                   dev(pk.block_table), dev(pk.seq_lens), dev(pk.v_tail), pk.seq_lens.tolist(), pk.dim, pk.layout,
+                   pk.block_x, pk.block_y, pk.page_tokens, pk.k_format)
+
+    @property
+    def batch(self) -> int:
+        return len(self.lens)
+
+    @property
+    def kv_heads(self) -> int:
+        return self.k_pages.shape[1]
+
+
+def paged_params(cache: DevicePagedKV, query_heads: int, tile: int | None = None, cu_count: int = 256) -> AkvPagedParams:
+    """Tile default: about one round of resident workgroups over the whole
+    ragged batch (in steps of lcm(16, block_y) tokens), within the kernel's
+    limit of 62 pages per split."""
+    P, by = cache.page_tokens, cache.block_y
+    step = 16
+    while step % by:
+        step += 16
+    max_t = max(cache.lens)
+    if tile is None:
+        groups = (3 if cache.dim == 64 else 2) * cu_count
+        want = -(-sum(cache.lens) * cache.kv_heads // groups)
+        tile = max(step, -(-want // step) * step)
+        limit = (62 * P) // step * step
+        while (tile + P) * P >= 1 << 24:
+            limit -= step
+            tile = min(tile, limit)
+        tile = min(tile, limit, -(-max_t // step) * step)
+    cols = cache.v_blocks.shape[3]
+    return AkvPagedParams(cache.batch, max_t, query_heads, cache.kv_heads, cache.dim, P, cache.block_table.shape[1],
+                          cache.k_pages.shape[0], tile, -(-max_t // tile), LAYOUTS[cache.layout], cache.block_x,
+                          by, cols, K_FORMATS[cache.k_format])
+
+
+def paged_task_tokens(params: AkvPagedParams) -> int:
+    rc = lib().akv_hip_paged_task_tokens(ct.byref(params))
+    if rc < 0:
+        _check(rc)
+    return rc
+
+
+def paged_decode_attention(q: torch.Tensor, cache: DevicePagedKV, params: AkvPagedParams | None = None,
+                           tile: int | None = None, partial=None, stats=None, out=None,
+                           return_states: bool = False):
+    """One decode step over a ragged batch: q [B,Hq,D] f32 -> out [B,Hq,D] f32."""
+    b, hq, d = q.shape
+    if b != cache.batch or d != cache.dim or hq % cache.kv_heads:
+        raise ValueError("q does not match the paged cache")
+    _need(q, torch.float32, "q")
+    if params is None:
+        params = paged_params(cache, hq, tile)
+    s = params.splits
+    if partial is None:
+        partial = torch.empty((b, hq, s, d), dtype=torch.float32, device=q.device)
+    if stats is None:
+        stats = torch.empty((b, hq, s, 2), dtype=torch.float32, device=q.device)
+    if out is None:
+        out = torch.empty((b, hq, d), dtype=torch.float32, device=q.device)
+    _check(lib().akv_hip_paged_decode_attention(
+        ct.byref(params), _ptr(q), _ptr(cache.k_pages), _ptr(cache.k_meta), _ptr(cache.v_blocks),
+        _ptr(cache.v_scale), _ptr(cache.v_offset), _ptr(cache.block_table), _ptr(cache.seq_lens),
+        _ptr(cache.v_tail), _ptr(partial), _ptr(stats), _ptr(out), _ptr(arrivals(q.device, b * cache.kv_heads)),
+        _stream(q.device)))
+    return (out, partial, stats) if return_states else out

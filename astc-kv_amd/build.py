@@ -23,7 +23,7 @@ HIP = HERE / "csrc" / "hip"
 INCLUDE = ROOT / "include"
 
 CODEC_SOURCES = ["astc_format.cpp", "astc_decode.cpp", "astc_encode.cpp", "bridge.cpp"]
-HIP_SOURCES = [HIP / "decode_attention.hip", CODEC / "astc_format.cpp"]
+HIP_SOURCES = [HIP / "decode_attention.hip", HIP / "paged_attention.hip", CODEC / "astc_format.cpp"]
 ARCH = os.environ.get("PYTORCH_ROCM_ARCH", "gfx950")
 
 
@@ -47,12 +47,23 @@ def build_cpu():
 
 
 def build_hip():
+    """Each source compiled to an object in parallel (the kernel translation
+    units take a minute or more each), then linked."""
+    from concurrent.futures import ThreadPoolExecutor
+
     out = PKG / "libastckv_hip.so"
     tmp = out.with_suffix(".so.tmp")
-    run([hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
-         # Packed FP32 instructions are kept out of every kernel.
-         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-         f"-I{INCLUDE}", f"-I{CODEC}", f"-I{HIP}", *HIP_SOURCES, "-o", tmp])
+    objdir = HERE / "_build"
+    objdir.mkdir(exist_ok=True)
+    flags = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+             # Packed FP32 instructions are kept out of every kernel.
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             f"-I{INCLUDE}", f"-I{CODEC}", f"-I{HIP}"]
+    objs = [objdir / (src.stem + ".o") for src in HIP_SOURCES]
+    with ThreadPoolExecutor(max_workers=len(HIP_SOURCES)) as pool:
+        for f in [pool.submit(run, [hipcc(), *flags, "-c", src, "-o", obj]) for src, obj in zip(HIP_SOURCES, objs)]:
+            f.result()
+    run([hipcc(), f"--offload-arch={ARCH}", "-fPIC", "-shared", *objs, "-o", tmp])
     tmp.replace(out)
     return out
 

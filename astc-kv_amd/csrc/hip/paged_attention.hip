@@ -1,0 +1,416 @@
+// Split-K decode attention over a paged, ragged batch for gfx950: K (FP16 or
+// 4-bit in groups of 32 channels) and ASTC V live in page pools addressed
+// through per-sequence block tables; an optional FP16 V tail holds each
+// sequence's tokens past its last full page. One launch per step: the last
+// split workgroup of each (sequence, kv head) merges.
+//
+// The schedule is the contiguous split kernel's (decode_attention.hip): chunks
+// of whole block rows, a header stage of one lane per block sorted by
+// decode-path class, groups of 16-token tiles on the matrix cores. What
+// changes is addressing: every block row, K row and scale/offset is found
+// through the split's pages (cached in LDS), chunks and tiles are aligned to
+// 16 tokens so that a tile never straddles a page, and tiles past the last
+// full page read V from the FP16 tail with scale 1 and offset 0.
+//
+// Reference semantics: metal/attention_gqa_v10.metal:568-674 and :229-253 (as
+// the contiguous kernel); 4-bit K as affine_quantize(axis="token", group=32),
+// astc_kv/codec.py:218-250. The reference has no paged kernel; its paged
+// format is a plan (docs/representation_v0.1.md:47-50, :84-95).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "astc_decode_device.h"
+#include "astc_format.h"
+#include "astc_kv_hip.h"
+#include "attention_device.h"
+#include "host_common.h"
+
+namespace akv_hip {
+namespace {
+
+constexpr int kMaxSplitPages = 64;   // pages one split may touch
+
+struct PagedArgs {
+    AkvPagedParams p;
+    Footprint fp;
+    uint32_t chunk_tokens;             // a multiple of 16 and of block_y
+    uint32_t rows_per_page;            // page_tokens / block_y
+    uint32_t mag_by, mag_bx, mag_cols, mag_page, mag_rpp;   // ceil(2^24 / divisor)
+    float qscale;
+};
+
+template <int D, int NCH>
+struct PagedShared {
+    AstcShared<D, NCH> a;
+    int32_t pages[kMaxSplitPages];     // the split's pages, from its first
+};
+
+// V of one texel column group from the FP16 tail, in the texel operand order
+// (RGBA: channels 4x .. 4x+3 of column x; scalar: channel x), for the four
+// tokens tail rows r[0..3].
+template <int D, int NCH>
+__device__ inline void tail_texels(const uint16_t* __restrict__ tail, const int (&r)[4], int x, uint2 (&tv)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (NCH == 4) tv[i] = *reinterpret_cast<const uint2*>(tail + size_t(r[i]) * D + 4 * x);
+        else tv[i] = uint2{uint32_t(tail[size_t(r[i]) * D + x]), 0u};
+    }
+}
+
+template <int D, int NCH, int G, bool KU4>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 64 ? AKV_ASTC_WAVES : 2))) void
+paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restrict__ kpool,
+                  const uint16_t* __restrict__ kmeta, const uint4* __restrict__ vpool,
+                  const uint16_t* __restrict__ vscale, const uint16_t* __restrict__ voffset,
+                  const int32_t* __restrict__ table, const int32_t* __restrict__ lens,
+                  const uint16_t* __restrict__ vtail, const AkvTables* __restrict__ tab, float* partial,
+                  float2* stats, float* __restrict__ out, uint32_t* arrivals) {
+    using C = Cfg<D, NCH>;
+    constexpr int TPG = Grp<G, D>::TPG;
+    constexpr int kKEarly = TPG < 2 ? TPG : 2;
+    // Per tile and lane: FP16 K, D/32 16-byte row pieces; 4-bit K, D/32 code
+    // dwords and D/32 (offset, scale) dwords.
+    constexpr int kKWords = KU4 ? D / 16 : 4 * (D / 32);
+    __shared__ PagedShared<D, NCH> shp;
+    AstcShared<D, NCH>& sh = shp.a;
+    const AkvPagedParams& p = a.p;
+    const Footprint f = a.fp;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int n16 = lane & 15, g = lane >> 4;
+    const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+    const int len = lens[b];
+    const int P = int(p.page_tokens);
+    const int split_begin = split * int(p.tile_tokens);
+    if (split_begin >= len) return;   // this sequence has fewer splits (uniform, before any barrier)
+    const int split_end = min(split_begin + int(p.tile_tokens), len);
+    const int full = vtail ? len - len % P : len;   // tokens whose V is in ASTC pages
+    const int page0 = split_begin / P, base_tok = page0 * P;
+    const int npages = (split_end - 1) / P - page0 + 1;
+    const int CT = int(a.chunk_tokens), by = f.by;
+    const int cols = int(p.atlas_cols), rpp = int(a.rows_per_page), Hkv = int(p.kv_heads);
+    const int32_t* seq_table = table + size_t(b) * p.max_pages + page0;
+    const uint16_t* tail = vtail ? vtail + (size_t(b) * Hkv + kh) * P * D : nullptr;
+
+    // Page of a token: (page id, token within the page); t_abs - base_tok < tile + page.
+    auto page_of = [&](int t_abs, int& pid, int& pos) {
+        const int rel = t_abs - base_tok;
+        const int pg = int(fdiv(uint32_t(rel), a.mag_page));
+        pid = shp.pages[pg];
+        pos = rel - pg * P;
+    };
+    auto chunk_astc = [&](int c0) { return max(0, min(full - c0, min(CT, split_end - c0))); };
+    auto chunk_blocks = [&](int c0) { return (chunk_astc(c0) + by - 1) / by * cols; };
+    // This lane's block of the chunk at c0 (nblk blocks); the first chunk reads
+    // its page ids from the block table, later ones from LDS.
+    auto load_blk = [&](int c0, int nblk, bool from_table) -> uint4 {
+        if (tid >= nblk) return uint4{0, 0, 0, 0};
+        const int r = int(fdiv(uint32_t(tid), a.mag_cols)), col = tid - r * cols;
+        const int grow = int(fdiv(uint32_t(c0 - base_tok), a.mag_by)) + r;
+        const int pg = int(fdiv(uint32_t(grow), a.mag_rpp)), prow = grow - pg * rpp;
+        const int pid = from_table ? seq_table[pg] : shp.pages[pg];
+        return vpool[((size_t(pid) * Hkv + kh) * rpp + prow) * cols + col];
+    };
+
+    uint4 raw = load_blk(split_begin, chunk_blocks(split_begin), true);
+    uint4 pw = tid < chunk_blocks(split_begin) ? partition_words(raw, tab) : uint4{0, 0, 0, 0};
+    if (tid < npages) shp.pages[tid] = seq_table[tid];
+    stage_tables(tab, sh.tabs, tid, kThreads);
+    if (tid < kPathKeys) sh.key_count[tid] = 0;
+    if (wave == 0) store_q<D, G>(q + (size_t(b) * p.query_heads + size_t(kh) * G) * D, a.qscale, &sh.q[0][0]);
+
+    int bcol[C::kColGroups], xin[C::kColGroups];
+#pragma unroll
+    for (int kc = 0; kc < C::kColGroups; ++kc) {
+        const int x = n16 + 16 * kc;
+        bcol[kc] = int(fdiv(uint32_t(x), a.mag_bx));
+        xin[kc] = x - bcol[kc] * f.bx;
+    }
+
+    AttnState<D> st;
+    st.m = -INFINITY;
+    st.l = st.off = 0.0f;
+#pragma unroll
+    for (int mb = 0; mb < C::kMBlocks; ++mb) st.o[mb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // K rows of the 16-token tile at chunk token t0 of the chunk at c0 (rows
+    // past the split read its last token; their scores are never used).
+    uint32_t kw[TPG * kKWords];
+    auto load_k = [&](uint32_t* r, int c0, int t0) {
+        int pid, pos;
+        page_of(min(c0 + t0 + n16, split_end - 1), pid, pos);
+        const size_t row = (size_t(pid) * Hkv + kh) * P + pos;
+        if constexpr (KU4) {
+            const uint8_t* codes = static_cast<const uint8_t*>(kpool) + row * (D / 2);
+#pragma unroll
+            for (int L = 0; L < D / 32; ++L) {
+                r[L] = *reinterpret_cast<const uint32_t*>(codes + 16 * L + 4 * g);
+                r[D / 32 + L] = *reinterpret_cast<const uint32_t*>(kmeta + (row * (D / 32) + L) * 2);
+            }
+        } else {
+            const uint16_t* k16 = static_cast<const uint16_t*>(kpool) + row * D;
+#pragma unroll
+            for (int L = 0; L < D / 32; ++L) {
+                const uint4 v = *reinterpret_cast<const uint4*>(k16 + 32 * L + 8 * g);
+                r[4 * L] = v.x;
+                r[4 * L + 1] = v.y;
+                r[4 * L + 2] = v.z;
+                r[4 * L + 3] = v.w;
+            }
+        }
+    };
+
+    __syncthreads();   // pages, decode tables and Q operands
+    for (int c0 = split_begin; c0 < split_end; c0 += CT) {
+        const int ntok = min(CT, split_end - c0);
+        const int ntiles = (ntok + 15) >> 4;
+        const int nastc = chunk_astc(c0);
+        const int nblk = chunk_blocks(c0);
+        // 1. Loads: the first K tiles of this wave's first group, per-token
+        // scale/offset (tail tokens: 1 and 0), the next chunk's blocks.
+#pragma unroll
+        for (int t = 0; t < kKEarly; ++t) load_k(kw + t * kKWords, c0, 16 * (TPG * wave + t));
+        static_assert(C::kMaxTok <= 2 * kThreads, "two scale/offset tokens per lane");
+        uint32_t so[2] = {0, 0};
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int t = tid + i * kThreads;
+            if (t < ntok) {
+                if (c0 + t < full) {
+                    int pid, pos;
+                    page_of(c0 + t, pid, pos);
+                    const size_t at = (size_t(pid) * Hkv + kh) * P + pos;
+                    so[i] = uint32_t(vscale[at]) | (uint32_t(voffset[at]) << 16);
+                } else {
+                    so[i] = 0x3C00u;   // fp16 1.0, offset 0
+                }
+            }
+        }
+        const uint4 raw_now = raw;
+        if (c0 + CT < split_end) raw = load_blk(c0 + CT, chunk_blocks(c0 + CT), false);
+        // 2. Block headers (the blocks of the chunk's ASTC tokens), sorted by
+        // decode-path class.
+        int key = 0, rank = 0;
+        if (tid < nblk) {
+            key = block_path_key(raw_now, sh.tabs);
+            stash_block(sh.u.h.desc[tid], raw_now, pw);
+            rank = int(atomicAdd(&sh.key_count[key], 1u));
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            if (tid + i * kThreads < 16 * ntiles) sh.so[tid + i * kThreads] = so[i];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            if (tid + i * kThreads < C::kMaxTok)
+                sh.tokrow[tid + i * kThreads] =
+                    token_row_entry(tid + i * kThreads, max(nastc, 1), a.mag_by, f, uint32_t(cols));
+        __syncthreads();
+        if (wave == 0) {   // exclusive scan of the class counts (kPathKeys == 64 lanes)
+            const uint32_t c = sh.key_count[lane];
+            uint32_t incl = c;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const uint32_t t = __shfl_up(incl, d, 64);
+                if (lane >= d) incl += t;
+            }
+            sh.key_base[lane] = incl - c;
+            sh.key_count[lane] = 0;
+        }
+        __syncthreads();
+        if (tid < nblk) sh.order[sh.key_base[key] + rank] = uint8_t(tid);
+        __syncthreads();
+        if (tid < nblk) decode_header<NCH>(sh.tabs, sh.u.h.desc[sh.order[tid]], sh.u.h.cv[tid]);
+        if (c0 + CT < split_end)
+            pw = tid < chunk_blocks(c0 + CT) ? partition_words(raw, tab) : uint4{0, 0, 0, 0};
+        __syncthreads();
+        // 3. Tile groups; tiles at or past `full` read V from the FP16 tail.
+#pragma unroll
+        for (int t = kKEarly; t < TPG; ++t) load_k(kw + t * kKWords, c0, 16 * (TPG * wave + t));
+#pragma unroll 1
+        for (int tb0 = 16 * TPG * wave; tb0 < ntok; tb0 += 16 * TPG * kWaves) {
+            const int ng = min(TPG, (ntok - tb0 + 15) >> 4);
+            uint32_t rows[4];
+            int trow[4];
+            bool in_tail = false;
+            auto vtile = [&](int t, int kc, half4* va) {
+                if (kc == 0) {
+                    if (t == 0) {   // S is done with this group's K rows
+                        const int nb0 = tb0 + 16 * TPG * kWaves;
+#pragma unroll
+                        for (int tt = 0; tt < TPG; ++tt) load_k(kw + tt * kKWords, c0, nb0 + 16 * tt);
+                    }
+                    in_tail = c0 + tb0 + 16 * t >= full;
+                    if (in_tail) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) trow[i] = min(c0 + tb0 + 16 * t + 4 * g + i, split_end - 1) - full;
+                    } else {
+                        tile_rows(sh.tokrow, tb0 + 16 * t, g, rows);
+                    }
+                }
+                uint2 tv[4];
+                if (in_tail) tail_texels<D, NCH>(tail, trow, n16 + 16 * kc, tv);
+                else column_texels<NCH>(sh.u.h.desc, sh.tabs, f, rows, bcol[kc], xin[kc], tv);
+                texel_operands<NCH>(tv, va);
+            };
+            if constexpr (KU4)
+                attend_group<D, G, true, C::kRowBlocksPerGroup>(U4KOperands<D>{kw}, &sh.q[0][0], ng, tb0, ntok,
+                                                                 sh.so, C::kMaxTok, st, vtile);
+            else
+                attend_group<D, G, true, C::kRowBlocksPerGroup>(
+                    Fp16KOperands<D>{reinterpret_cast<const uint4*>(kw)}, &sh.q[0][0], ng, tb0, ntok, sh.so,
+                    C::kMaxTok, st, vtile);
+        }
+        __syncthreads();   // descriptors and so are rewritten by the next chunk
+    }
+    const size_t qh0 = size_t(b) * p.query_heads + size_t(kh) * G;
+    const int S = int(p.splits), Sb = (len + int(p.tile_tokens) - 1) / int(p.tile_tokens);
+    combine_waves<D, NCH, G>(sh.u.comb, sh.ws, st, partial, stats, qh0, S, split);
+    merge_if_last<D, G>(arrivals + size_t(b) * Hkv + kh, partial, stats, out, qh0, Sb, S, sh.ws, sh.u.comb,
+                        kWaves * D * kMaxG);
+}
+
+// --- host ---------------------------------------------------------------------
+
+int check_paged(const AkvPagedParams* p, uint32_t* G) {
+    if (!p) return AKV_HIP_ERR_NULL;
+    if (p->batch == 0 || p->max_tokens == 0 || p->kv_heads == 0 || p->query_heads % p->kv_heads)
+        return AKV_HIP_ERR_SHAPE;
+    if (p->dim != 64 && p->dim != 128) return AKV_HIP_ERR_SHAPE;
+    const uint32_t g = p->query_heads / p->kv_heads;
+    if (g != 1 && g != 2 && g != 3 && g != 4 && g != 8) return AKV_HIP_ERR_SHAPE;
+    if (p->batch > 65535 || p->kv_heads > 65535 || p->num_pages == 0) return AKV_HIP_ERR_SHAPE;
+    if (p->k_format != AKV_K_FP16 && p->k_format != AKV_K_U4G32) return AKV_HIP_ERR_SHAPE;
+    if (p->layout != AKV_LAYOUT_SCALAR && p->layout != AKV_LAYOUT_RGBA) return AKV_HIP_ERR_SHAPE;
+    const uint32_t bx = p->block_x, by = p->block_y;
+    if (bx < 4 || by < 4 || bx > 12 || by > 12 || bx * by > uint32_t(akv::kMaxTexels)) return AKV_HIP_ERR_FOOTPRINT;
+    const uint32_t texcols = p->layout == AKV_LAYOUT_SCALAR ? p->dim : p->dim / 4;
+    if (p->atlas_cols != (texcols + bx - 1) / bx) return AKV_HIP_ERR_SHAPE;
+    const uint32_t P = p->page_tokens;
+    if (P == 0 || P % 16 || P % by || P > 4096) return AKV_HIP_ERR_SHAPE;
+    if (uint64_t(p->max_pages) * P < p->max_tokens) return AKV_HIP_ERR_SHAPE;
+    const uint32_t T = p->tile_tokens;
+    if (T == 0 || T % 16 || T % by) return AKV_HIP_ERR_TILE;
+    if (p->splits != (p->max_tokens + T - 1) / T || p->splits > 2147483647u) return AKV_HIP_ERR_TILE;
+    // Pages a split touches; split-relative offsets times the divisors fit 24 bits.
+    if ((T + P - 1) / P + 1 > uint32_t(kMaxSplitPages) || uint64_t(T + P) * P >= (1u << 24))
+        return AKV_HIP_ERR_TILE;
+    *G = g;
+    return 0;
+}
+
+// Chunk: the most 16-token-aligned whole block rows (a multiple of
+// lcm(16, block_y) tokens) whose blocks fit the header stage.
+template <int D, int NCH>
+int plan_paged(const AkvPagedParams* p, PagedArgs* a) {
+    using C = Cfg<D, NCH>;
+    const uint32_t by = p->block_y;
+    uint32_t step = 16;
+    while (step % by) step += 16;
+    uint32_t rows = uint32_t(C::kMaxBlocks) / p->atlas_cols;
+    uint32_t tokens = rows * by;
+    if (tokens > uint32_t(C::kMaxTok)) tokens = uint32_t(C::kMaxTok);
+    tokens -= tokens % step;
+    if (tokens == 0) return AKV_HIP_ERR_SHAPE;
+    a->chunk_tokens = tokens < p->tile_tokens ? tokens : p->tile_tokens;
+    return 0;
+}
+
+int make_paged_args(const AkvPagedParams* p, PagedArgs* a) {
+    *a = PagedArgs{};
+    a->p = *p;
+    a->fp = footprint(p->block_x, p->block_y);
+    a->rows_per_page = p->page_tokens / p->block_y;
+    a->mag_by = magic(p->block_y);
+    a->mag_bx = magic(p->block_x);
+    a->mag_cols = magic(p->atlas_cols);
+    a->mag_page = magic(p->page_tokens);
+    a->mag_rpp = magic(a->rows_per_page);
+    a->qscale = float(1.4426950408889634 / std::sqrt(double(p->dim)));
+    const bool scalar = p->layout == AKV_LAYOUT_SCALAR;
+    if (p->dim == 64) return scalar ? plan_paged<64, 1>(p, a) : plan_paged<64, 4>(p, a);
+    return scalar ? plan_paged<128, 1>(p, a) : plan_paged<128, 4>(p, a);
+}
+
+struct PagedPtrs {
+    const float* q;
+    const void* k;
+    const uint16_t* kmeta;
+    const uint4* v;
+    const uint16_t* vs;
+    const uint16_t* vo;
+    const int32_t* table;
+    const int32_t* lens;
+    const uint16_t* tail;
+    const AkvTables* tab;
+    float* partial;
+    float2* stats;
+    float* out;
+    uint32_t* arrivals;
+};
+
+template <int D, int NCH, bool KU4>
+hipError_t launch_paged_g(const PagedArgs& a, uint32_t G, const PagedPtrs& x, hipStream_t st) {
+    dim3 grid(a.p.splits, a.p.kv_heads, a.p.batch);
+    switch (G) {
+#define AKV_CASE(GG)                                                                                          \
+    case GG:                                                                                                  \
+        paged_attn_kernel<D, NCH, GG, KU4><<<grid, kThreads, 0, st>>>(a, x.q, x.k, x.kmeta, x.v, x.vs, x.vo,  \
+                                                                      x.table, x.lens, x.tail, x.tab,        \
+                                                                      x.partial, x.stats, x.out, x.arrivals); \
+        break;
+        AKV_CASE(1)
+        AKV_CASE(2)
+        AKV_CASE(3)
+        AKV_CASE(4)
+        AKV_CASE(8)
+#undef AKV_CASE
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <bool KU4>
+hipError_t launch_paged(const PagedArgs& a, uint32_t G, const PagedPtrs& x, hipStream_t st) {
+    const bool scalar = a.p.layout == AKV_LAYOUT_SCALAR;
+    if (a.p.dim == 64)
+        return scalar ? launch_paged_g<64, 1, KU4>(a, G, x, st) : launch_paged_g<64, 4, KU4>(a, G, x, st);
+    return scalar ? launch_paged_g<128, 1, KU4>(a, G, x, st) : launch_paged_g<128, 4, KU4>(a, G, x, st);
+}
+
+}  // namespace
+}  // namespace akv_hip
+
+using namespace akv_hip;
+
+extern "C" {
+
+int akv_hip_paged_decode_attention(const AkvPagedParams* p, const float* q, const void* k_pages,
+                                   const uint16_t* k_meta, const void* v_blocks, const uint16_t* v_scale,
+                                   const uint16_t* v_offset, const int32_t* block_table, const int32_t* seq_lens,
+                                   const uint16_t* v_tail, float* partial, float* stats, float* out,
+                                   uint32_t* arrivals, void* stream) {
+    uint32_t G = 0;
+    if (int rc = check_paged(p, &G)) return rc;
+    if (!q || !k_pages || !v_blocks || !v_scale || !v_offset || !block_table || !seq_lens || !partial || !stats ||
+        !out || !arrivals || (p->k_format == AKV_K_U4G32 && !k_meta))
+        return AKV_HIP_ERR_NULL;
+    const AkvTables* tab = nullptr;
+    if (int rc = device_tables(int(p->block_x), int(p->block_y), &tab)) return rc;
+    PagedArgs a;
+    if (int rc = make_paged_args(p, &a)) return rc;
+    const PagedPtrs x{q, k_pages, k_meta, static_cast<const uint4*>(v_blocks), v_scale, v_offset, block_table,
+                      seq_lens, v_tail, tab, partial, reinterpret_cast<float2*>(stats), out, arrivals};
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    return as_int(p->k_format == AKV_K_U4G32 ? launch_paged<true>(a, G, x, st) : launch_paged<false>(a, G, x, st));
+}
+
+int akv_hip_paged_task_tokens(const AkvPagedParams* p) {
+    uint32_t G = 0;
+    if (int rc = check_paged(p, &G)) return rc;
+    PagedArgs a;
+    if (int rc = make_paged_args(p, &a)) return rc;
+    return int(a.chunk_tokens);
+}
+
+}  // extern "C"

@@ -127,6 +127,62 @@ int akv_hip_decode_blocks(const void* blocks, size_t n, unsigned bx, unsigned by
    (astc != 0) or for the FP16 control, or a negative AKV_HIP_* code. */
 int akv_hip_task_tokens(const AkvAttnParams* p, int astc);
 
+/* --- Paged, ragged batches ---------------------------------------------------
+ *
+ * Sequences of different lengths whose K and V live in page pools addressed
+ * through per-sequence block tables (the paged format the reference plans,
+ * docs/representation_v0.1.md:47-50, :84-95). A page holds page_tokens tokens
+ * of every kv head. Pools, for num_pages pages:
+ *   k_pages   AKV_K_FP16: fp16 [num_pages][kv_heads][page_tokens][dim]
+ *             AKV_K_U4G32: 4-bit codes [num_pages][kv_heads][page_tokens][dim/2]
+ *             (two per byte, low nibble = even channel), with
+ *   k_meta    fp16 [num_pages][kv_heads][page_tokens][dim/32][2] = (offset,
+ *             scale) per group of 32 channels: k = code * scale + offset
+ *             (affine_quantize(axis="token", group=32), codec.py:218-250)
+ *   v_blocks  16-byte ASTC blocks [num_pages][kv_heads][page_tokens/block_y][atlas_cols]
+ *   v_scale, v_offset  fp16 [num_pages][kv_heads][page_tokens]
+ *   block_table int32 [batch][max_pages]: page of each page_tokens tokens
+ *   seq_lens  int32 [batch], 1 .. max_tokens
+ *   v_tail    NULL, or fp16 [batch][kv_heads][page_tokens][dim]: the last
+ *             seq_len % page_tokens tokens of each sequence take V from here
+ *             (the fresh tail not yet encoded; their pages' V blocks are not
+ *             read), tail token i at row i.
+ * Split states partial/stats are laid out as in the contiguous API with
+ * `splits` = ceil(max_tokens / tile_tokens); sequence b uses its first
+ * ceil(seq_len / tile_tokens). `arrivals`: batch * kv_heads zeroed counters,
+ * as akv_hip_decode_attention_fused (the merge always runs in the split
+ * launch here). No reference counterpart: the reference only sketches pages. */
+#define AKV_K_FP16 0u
+#define AKV_K_U4G32 1u
+
+typedef struct AkvPagedParams {
+    uint32_t batch;
+    uint32_t max_tokens;    /* longest sequence */
+    uint32_t query_heads;
+    uint32_t kv_heads;
+    uint32_t dim;           /* 64 or 128 */
+    uint32_t page_tokens;   /* a multiple of 16 and of block_y */
+    uint32_t max_pages;     /* block_table row length, >= ceil(max_tokens / page_tokens) */
+    uint32_t num_pages;     /* pages in each pool */
+    uint32_t tile_tokens;   /* tokens per split: a multiple of 16 and of block_y */
+    uint32_t splits;        /* ceil(max_tokens / tile_tokens) */
+    uint32_t layout;        /* AKV_LAYOUT_SCALAR or AKV_LAYOUT_RGBA */
+    uint32_t block_x;
+    uint32_t block_y;
+    uint32_t atlas_cols;    /* blocks per page row */
+    uint32_t k_format;      /* AKV_K_FP16 or AKV_K_U4G32 */
+} AkvPagedParams;
+
+int akv_hip_paged_decode_attention(const AkvPagedParams* p, const float* q, const void* k_pages,
+                                   const uint16_t* k_meta, const void* v_blocks, const uint16_t* v_scale,
+                                   const uint16_t* v_offset, const int32_t* block_table, const int32_t* seq_lens,
+                                   const uint16_t* v_tail, float* partial, float* stats, float* out,
+                                   uint32_t* arrivals, void* stream);
+
+/* Host-side planning query for the paged kernel (no GPU work): tokens per
+   chunk, or a negative AKV_HIP_* code. */
+int akv_hip_paged_task_tokens(const AkvPagedParams* p);
+
 /* Text for a return code of the functions above. */
 const char* akv_hip_error_string(int code);
 

@@ -1,0 +1,91 @@
+"""Paged, ragged decode attention (akv_hip_paged_decode_attention) against the
+NumPy oracle, per sequence, on K and V reconstructed on the host from the
+pages each block-table row names: FP16 or 4-bit K (code * scale + offset in
+float32, astc_kv/codec.py:248), V restored from the oracle's decode of the
+page blocks plus the FP16 tail. Tolerance as test_gpu_attention: rtol 1e-3 /
+atol 2e-3 against the fp32 oracle, relative L2 <= 1e-4 against FP64."""
+import numpy as np
+import pytest
+
+from oracle import astc_oracle as O
+from oracle import attention_ref as R
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+RTOL, ATOL, REL_L2 = 1e-3, 2e-3, 1e-4
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    from astc_kv import gpu as G
+    G.lib()
+    return G
+
+
+def host_kv(pk, i):
+    """K and V of sequence i as float32 [Hkv, T, D], read back through its pages."""
+    t, P, h, d = int(pk.seq_lens[i]), pk.page_tokens, pk.kv_heads, pk.dim
+    ids = pk.block_table[i, :-(-t // P)]
+    if pk.k_format == "fp16":
+        k = pk.k_pages[ids].transpose(1, 0, 2, 3).reshape(h, -1, d)[:, :t].astype(np.float32)
+    else:
+        b = pk.k_pages[ids].transpose(1, 0, 2, 3).reshape(h, -1, d // 2)[:, :t]
+        codes = np.stack([b & 15, b >> 4], -1).reshape(h, t, d // 32, 32).astype(np.float32)
+        meta = pk.k_meta[ids].transpose(1, 0, 2, 3, 4).reshape(h, -1, d // 32, 2)[:, :t].astype(np.float32)
+        k = (codes * meta[..., 1:2] + meta[..., 0:1]).reshape(h, t, d)
+    full = pk.full_tokens(i)
+    parts = []
+    if full:
+        npg = -(-full // P)
+        rpp, cols, bx, by = P // pk.block_y, pk.cols, pk.block_x, pk.block_y
+        blocks = pk.v_blocks[ids[:npg]].transpose(1, 0, 2, 3, 4).reshape(h, npg * rpp, cols, 16)
+        tex, _ = O.decode_blocks_fp16(np.ascontiguousarray(blocks).reshape(-1, 16), bx, by)
+        img = tex.reshape(h, npg * rpp, cols, by, bx, 4).transpose(0, 1, 3, 2, 4, 5)
+        img = img.reshape(h, npg * P, cols * bx, 4)[:, :full].astype(np.float32)
+        u = img[..., :d, 0] if pk.layout == "scalar" else img[:, :, : d // 4].reshape(h, full, d)
+        s = pk.v_scale[ids[:npg]].transpose(1, 0, 2).reshape(h, -1)[:, :full].astype(np.float32)
+        o = pk.v_offset[ids[:npg]].transpose(1, 0, 2).reshape(h, -1)[:, :full].astype(np.float32)
+        parts.append(R.restore_token(u, s[..., None], o[..., None]))
+    if full < t:
+        parts.append(pk.v_tail[i, :, : t - full].astype(np.float32))
+    return k, np.concatenate(parts, axis=1)
+
+
+CASES = [
+    # layout, block, page, dim, hq, hkv, k_format, tail
+    ("scalar", (6, 6), 96, 128, 8, 2, "u4g32", True),
+    ("rgba", (4, 4), 64, 128, 8, 2, "fp16", False),
+    ("rgba", (6, 5), 80, 64, 9, 3, "fp16", True),
+    ("scalar", (6, 6), 96, 64, 9, 3, "u4g32", True),
+    ("rgba", (8, 8), 64, 64, 8, 1, "u4g32", False),
+]
+
+
+@pytest.mark.parametrize("layout,block,page,d,hq,hkv,kf,tail", CASES)
+def test_paged_attention(gpu, layout, block, page, d, hq, hkv, kf, tail):
+    from astc_kv.paged import build_paged
+    rng = np.random.default_rng(page + d + hq)
+    lens = [100, 517, 1200, page, 333, 1]
+    k = []
+    for t in lens:
+        kk = rng.normal(size=(hkv, t, d))
+        kk[..., :4] *= 8.0
+        k.append(kk.astype(np.float16))
+    v = [rng.normal(0, 0.5, size=(hkv, t, d)).astype(np.float32) for t in lens]
+    pk = build_paged(k, v, layout, block, page, quality=20, k_format=kf, tail=tail, seed=len(lens))
+    cache = gpu.DevicePagedKV.from_host(pk)
+    q = rng.normal(size=(len(lens), hq, d)).astype(np.float32)
+    qt = torch.from_numpy(q).cuda()
+    step = 16
+    while step % block[1]:
+        step += 16
+    for tile in (None, 2 * step):
+        out = gpu.paged_decode_attention(qt, cache, tile=tile).cpu().numpy()
+        for i in range(len(lens)):
+            ki, vi = host_kv(pk, i)
+            ref = R.decode_attention(q[i:i + 1], ki[None], vi[None])[0]
+            np.testing.assert_allclose(out[i], ref, rtol=RTOL, atol=ATOL, err_msg=f"sequence {i} tile {tile}")
+            ref64 = R.attention_fp64(q[i], ki.astype(np.float64), vi)
+            assert R.relative_l2(ref64, out[i]) <= REL_L2
