@@ -71,9 +71,10 @@ class PagedKV:
 
 def build_paged(k_seqs, v_seqs, layout: str = "scalar", block=(6, 6), page_tokens: int = 96,
                 quality: float = 50, k_format: str = "fp16", tail: bool = True, seed: int = 0,
-                threads: int | None = None) -> PagedKV:
+                threads: int | None = None, progress=None) -> PagedKV:
     """k_seqs, v_seqs: per sequence [Hkv, T_i, D] (K fp16 or float, V float).
-    Pages are assigned in a seeded random order."""
+    Pages are assigned in a seeded random order. progress(i, n), if given, is
+    called after each sequence."""
     bx, by = codec._footprint(block)
     if page_tokens % 16 or page_tokens % by:
         raise ValueError("page_tokens must be a multiple of 16 and of the block height")
@@ -138,5 +139,7 @@ def build_paged(k_seqs, v_seqs, layout: str = "scalar", block=(6, 6), page_token
                 v_blocks[pid] = at.blocks[0, :, j * rpp:(j + 1) * rpp]
                 v_scale[pid] = at.scale[0, :, j * P:(j + 1) * P]
                 v_offset[pid] = at.offset[0, :, j * P:(j + 1) * P]
+        if progress is not None:
+            progress(i + 1, len(lens))
     return PagedKV(k_pages, k_meta, v_blocks, v_scale, v_offset, table, np.asarray(lens, np.int32), v_tail, d,
                    layout, bx, by, P, k_format)

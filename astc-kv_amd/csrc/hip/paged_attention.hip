@@ -106,7 +106,9 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
     auto load_blk = [&](int c0, int nblk, bool from_table) -> uint4 {
         if (tid >= nblk) return uint4{0, 0, 0, 0};
         const int r = int(fdiv(uint32_t(tid), a.mag_cols)), col = tid - r * cols;
-        const int grow = int(fdiv(uint32_t(c0 - base_tok), a.mag_by)) + r;
+        // (c0 - base_tok) / by can exceed the 8-bit quotients fdiv is exact
+        // for; c0 and base_tok are uniform, so this is one scalar division.
+        const int grow = (c0 - base_tok) / by + r;
         const int pg = int(fdiv(uint32_t(grow), a.mag_rpp)), prow = grow - pg * rpp;
         const int pid = from_table ? seq_table[pg] : shp.pages[pg];
         return vpool[((size_t(pid) * Hkv + kh) * rpp + prow) * cols + col];

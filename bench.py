@@ -76,6 +76,12 @@ def parse_args(argv=None):
     ap.add_argument("--summarize", nargs=3, metavar=("KT", "FETCH", "WRITE"),
                     help="print a markdown summary of rocprofv3 CSV output directories and exit")
     ap.add_argument("--out", default="", help="also write the JSON line to this file")
+    ap.add_argument("--ragged", type=int, default=0,
+                    help="paged ragged batch of this many sequences (lengths uniform in "
+                         "[--min-tokens, --tokens]) instead of the uniform batch")
+    ap.add_argument("--min-tokens", type=int, default=512)
+    ap.add_argument("--k-format", default="fp16", choices=["fp16", "u4g32"], help="K storage (paged batches)")
+    ap.add_argument("--tail", action="store_true", help="paged: keep each sequence's partial last page as FP16 V")
     return ap.parse_args(argv)
 
 
@@ -242,6 +248,113 @@ def summarize(kt_dir: str, fetch_dir: str, write_dir: str, calib_mb: float, work
     return text
 
 
+def ragged_workload_name(a) -> str:
+    bx, by = a.block.split("x")
+    return (f"paged decode attention, ragged batch of {a.ragged} (T uniform in [{a.min_tokens},{a.tokens}]), "
+            f"{a.query_heads}q/{a.kv_heads}kv, D{a.dim}, {a.k_format} K + ASTC {a.layout.upper()} {bx}x{by} V "
+            f"(page {a.page}{', FP16 tail' if a.tail else ''}), block tables")
+
+
+def main_ragged(a, torch, gpu):
+    """A ragged batch in page pools with block tables (akv_hip_paged_decode_attention)."""
+    from astc_kv.paged import build_paged
+    from oracle import astc_oracle as O
+    from oracle import attention_ref as R
+
+    bx, by = (int(x) for x in a.block.split("x"))
+    rng = np.random.default_rng(20261202)
+    lens = rng.integers(a.min_tokens, a.tokens + 1, size=a.ragged).tolist()
+    log(f"building {a.ragged} paged sequences, {sum(lens)} tokens: {ragged_workload_name(a)}")
+    t0 = time.perf_counter()
+    k, v = [], []
+    for t in lens:
+        kk = rng.normal(size=(a.kv_heads, t, a.dim)).astype(np.float32)
+        kk[..., :4] *= 8.0
+        k.append(kk.astype(np.float16))
+        v.append(rng.normal(0.0, 0.5, size=(a.kv_heads, t, a.dim)).astype(np.float32))
+    pk = build_paged(k, v, a.layout, (bx, by), a.page, a.quality, a.k_format, a.tail, seed=7,
+                     progress=lambda i, n: log(f"  encoded {i}/{n} sequences") if i % 8 == 0 or i == n else None)
+    setup_s = time.perf_counter() - t0
+    cache = gpu.DevicePagedKV.from_host(pk)
+    q = rng.normal(size=(a.ragged, a.query_heads, a.dim)).astype(np.float32)
+    qt = torch.from_numpy(q).cuda()
+    params = gpu.paged_params(cache, a.query_heads)
+    s = params.splits
+    partial = torch.empty((a.ragged, a.query_heads, s, a.dim), dtype=torch.float32, device="cuda")
+    stats = torch.empty((a.ragged, a.query_heads, s, 2), dtype=torch.float32, device="cuda")
+    out = torch.empty((a.ragged, a.query_heads, a.dim), dtype=torch.float32, device="cuda")
+    counts = pk.byte_counts()
+    step_bytes_ = counts["total"] + 2 * a.ragged * a.query_heads * a.dim * 4
+
+    def step(i):
+        gpu.paged_decode_attention(qt, cache, params=params, partial=partial, stats=stats, out=out)
+
+    log(f"timing {a.steps} steps (tile {params.tile_tokens}, {s} splits max)")
+    ms_step, mode = time_graph(torch, step, a.steps, a.warmup, not a.no_graph)
+
+    # Parity on the shortest and the longest sequence.
+    step(0)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    sub = [int(np.argmin(lens)), int(np.argmax(lens))]
+    max_err, parity = 0.0, True
+    for i in sub:
+        t, P, h, d = lens[i], a.page, a.kv_heads, a.dim
+        ids = pk.block_table[i, :-(-t // P)]
+        if a.k_format == "fp16":
+            ki = pk.k_pages[ids].transpose(1, 0, 2, 3).reshape(h, -1, d)[:, :t].astype(np.float32)
+        else:
+            kb = pk.k_pages[ids].transpose(1, 0, 2, 3).reshape(h, -1, d // 2)[:, :t]
+            codes = np.stack([kb & 15, kb >> 4], -1).reshape(h, t, d // 32, 32).astype(np.float32)
+            meta = pk.k_meta[ids].transpose(1, 0, 2, 3, 4).reshape(h, -1, d // 32, 2)[:, :t].astype(np.float32)
+            ki = (codes * meta[..., 1:2] + meta[..., 0:1]).reshape(h, t, d)
+        full = pk.full_tokens(i)
+        parts = []
+        if full:
+            npg, rpp, cols = -(-full // P), P // by, pk.cols
+            blocks = pk.v_blocks[ids[:npg]].transpose(1, 0, 2, 3, 4).reshape(h, npg * rpp, cols, 16)
+            tex, _ = O.decode_blocks_fp16(np.ascontiguousarray(blocks).reshape(-1, 16), bx, by)
+            img = tex.reshape(h, npg * rpp, cols, by, bx, 4).transpose(0, 1, 3, 2, 4, 5)
+            img = img.reshape(h, npg * P, cols * bx, 4)[:, :full].astype(np.float32)
+            u = img[..., :d, 0] if a.layout == "scalar" else img[:, :, : d // 4].reshape(h, full, d)
+            sc = pk.v_scale[ids[:npg]].transpose(1, 0, 2).reshape(h, -1)[:, :full].astype(np.float32)
+            of = pk.v_offset[ids[:npg]].transpose(1, 0, 2).reshape(h, -1)[:, :full].astype(np.float32)
+            parts.append(R.restore_token(u, sc[..., None], of[..., None]))
+        if full < t:
+            parts.append(pk.v_tail[i, :, : t - full].astype(np.float32))
+        ref = R.decode_attention(q[i:i + 1], ki[None], np.concatenate(parts, 1)[None])[0]
+        max_err = max(max_err, float(np.max(np.abs(got[i] - ref))))
+        parity = parity and bool(np.allclose(got[i], ref, rtol=1e-3, atol=2e-3))
+
+    value = step_bytes_ / (ms_step * 1e-3) / 1e9
+    line = {
+        "metric": "µs per decode-attention step + effective KV GB/s (% HBM peak)",
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 6), "us_per_step": round(ms_step * 1e3, 3),
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": f"{a.k_format} K / ASTC V (u16 texels), fp32 accumulate",
+        "data": "synthetic (seeded Gaussian K/V/q), V encoded by this package's ASTC encoder",
+        "config": {"workload": ragged_workload_name(a), "sequences": a.ragged, "tokens_total": int(sum(lens)),
+                   "tokens_max": int(max(lens)), "query_heads": a.query_heads, "kv_heads": a.kv_heads,
+                   "dim": a.dim, "layout": a.layout, "block": [bx, by], "page_tokens": a.page,
+                   "k_format": a.k_format, "tail": a.tail, "tile_tokens": params.tile_tokens,
+                   "splits_max": s, "timing": mode, "bytes_per_step": {**counts, "step": step_bytes_}},
+        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "paged_attn_kernel (split + in-kernel merge)", "bytes_per_launch": step_bytes_,
+                     "us_per_launch": round(ms_step * 1e3, 3)},
+        "cpu_baseline": None,
+        "parity": {"sequences_checked": sub, "max_abs_err": max_err, "within_rtol1e-3_atol2e-3": parity},
+        "setup_s": round(setup_s, 2),
+    }
+    text = json.dumps(line)
+    print(text, flush=True)
+    if a.out:
+        Path(a.out).parent.mkdir(parents=True, exist_ok=True)
+        Path(a.out).write_text(text + "\n")
+    return 0 if parity else 1
+
+
 def main(argv=None):
     a = parse_args(argv)
     if a.summarize:
@@ -254,6 +367,8 @@ def main(argv=None):
     import torch
 
     from astc_kv import gpu
+    if a.ragged:
+        return main_ragged(a, torch, gpu)
     from astc_kv.atlas import Atlas, build_atlas
     from oracle import astc_oracle as O
     from oracle import attention_ref as R

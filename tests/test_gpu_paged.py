@@ -89,3 +89,21 @@ def test_paged_attention(gpu, layout, block, page, d, hq, hkv, kf, tail):
             np.testing.assert_allclose(out[i], ref, rtol=RTOL, atol=ATOL, err_msg=f"sequence {i} tile {tile}")
             ref64 = R.attention_fp64(q[i], ki.astype(np.float64), vi)
             assert R.relative_l2(ref64, out[i]) <= REL_L2
+
+
+def test_long_splits_many_chunks(gpu):
+    """Splits of thousands of tokens: block rows far from the split's first page
+    (more than 255 rows, past the range of the 24-bit quotient helper)."""
+    from astc_kv.paged import build_paged
+    rng = np.random.default_rng(31)
+    lens = [3000, 2900, 97]
+    k = [rng.normal(size=(2, t, 128)).astype(np.float16) for t in lens]
+    v = [rng.normal(0, 0.5, size=(2, t, 128)).astype(np.float32) for t in lens]
+    pk = build_paged(k, v, "scalar", (6, 6), 96, quality=20, k_format="u4g32", tail=False, seed=1)
+    cache = gpu.DevicePagedKV.from_host(pk)
+    q = rng.normal(size=(len(lens), 8, 128)).astype(np.float32)
+    out = gpu.paged_decode_attention(torch.from_numpy(q).cuda(), cache, tile=2880).cpu().numpy()
+    for i in range(len(lens)):
+        ki, vi = host_kv(pk, i)
+        ref = R.decode_attention(q[i:i + 1], ki[None], vi[None])[0]
+        np.testing.assert_allclose(out[i], ref, rtol=RTOL, atol=ATOL, err_msg=f"sequence {i}")
