@@ -366,9 +366,10 @@ class DevicePagedKV:
 
 
 def paged_params(cache: DevicePagedKV, query_heads: int, tile: int | None = None, cu_count: int = 256) -> AkvPagedParams:
-    """Tile default: about one round of resident workgroups over the whole
-    ragged batch (in steps of lcm(16, block_y) tokens), within the kernel's
-    limit of 62 pages per split."""
+    """Tile default: about six rounds of resident workgroups over the whole
+    ragged batch (in steps of lcm(16, block_y) tokens; with uneven lengths
+    shorter splits balance the rounds), within the kernel's limit of 62 pages
+    per split."""
     P, by = cache.page_tokens, cache.block_y
     step = 16
     while step % by:
@@ -376,7 +377,7 @@ def paged_params(cache: DevicePagedKV, query_heads: int, tile: int | None = None
     max_t = max(cache.lens)
     if tile is None:
         groups = (3 if cache.dim == 64 else 2) * cu_count
-        want = -(-sum(cache.lens) * cache.kv_heads // groups)
+        want = -(-sum(cache.lens) * cache.kv_heads // (6 * groups))
         tile = max(step, -(-want // step) * step)
         limit = (62 * P) // step * step
         while (tile + P) * P >= 1 << 24:
