@@ -80,10 +80,32 @@ struct Footprint {
 };
 
 // Copy the decode tables into LDS (16-byte copies; `tab` is 256-byte aligned).
-__device__ inline void stage_tables(const AkvTables* __restrict__ tab, LdsTables& L, int tid, int nthreads) {
-    const uint4* src = reinterpret_cast<const uint4*>(tab);
-    uint4* dst = reinterpret_cast<uint4*>(&L);
-    for (int i = tid; i < int(sizeof(LdsTables) / 16); i += nthreads) dst[i] = src[i];
+// The copy in two halves, so that a kernel can issue the loads early and
+// store them after other work: every load is issued before the first store
+// (one memory latency, not one per pass), and the stores are unconditional
+// (lanes past the end rewrite the last entry with its own value; a guarded
+// store would let the compiler sink its load into the guard).
+template <int NT>
+struct TableStage {
+    static constexpr int kN = int(sizeof(LdsTables) / 16), kIter = (kN + NT - 1) / NT;
+    uint4 v[kIter];
+    __device__ void load(const AkvTables* __restrict__ tab, int tid) {
+        const uint4* src = reinterpret_cast<const uint4*>(tab);
+#pragma unroll
+        for (int j = 0; j < kIter; ++j) v[j] = src[min(tid + j * NT, kN - 1)];
+    }
+    __device__ void store(LdsTables& L, int tid) const {
+        uint4* dst = reinterpret_cast<uint4*>(&L);
+#pragma unroll
+        for (int j = 0; j < kIter; ++j) dst[min(tid + j * NT, kN - 1)] = v[j];
+    }
+};
+
+template <int NT>
+__device__ inline void stage_tables(const AkvTables* __restrict__ tab, LdsTables& L, int tid) {
+    TableStage<NT> t;
+    t.load(tab, tid);
+    t.store(L, tid);
 }
 
 // Bits [pos, pos + len) of a little-endian bit stream held in LDS dwords
@@ -462,8 +484,6 @@ __device__ inline void set_constant(BlockDesc<NCH>& d, uint32_t r, uint32_t g, u
     put_entry<NCH>(d.tab, 0, ep, weight_pair(0));
 #pragma unroll
     for (int i = 0; i < 5; ++i) d.qw[i] = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) d.part[i] = 0;
     d.info = kInfoTable | kInfoIdentity | (1u << kInfoLevelsShift);
 }
 
@@ -490,13 +510,13 @@ struct FieldWriter {
 
 // Before decode_header runs, a block waits in its own BlockDesc::tab:
 //   tab[0..3]   the 128-bit block, little endian;
-//   tab[4..7]   its partition_words;
 //   tab[8..11]  the block bit-reversed (the weight stream from bit 0), tab[12] = 0.
+// BlockDesc::part is not the header stage's: the lane that loaded the block
+// writes it (block_part_words) any time before the texel stage.
 template <int NCH>
-__device__ inline void stash_block(BlockDesc<NCH>& d, uint4 raw, uint4 pw) {
+__device__ inline void stash_block(BlockDesc<NCH>& d, uint4 raw) {
     uint4* t = reinterpret_cast<uint4*>(d.tab);
     t[0] = raw;
-    t[1] = pw;
     t[2] = uint4{__builtin_bitreverse32(raw.w), __builtin_bitreverse32(raw.z), __builtin_bitreverse32(raw.y),
                  __builtin_bitreverse32(raw.x)};
     d.tab[12] = 0;
@@ -506,7 +526,9 @@ __device__ inline void stash_block(BlockDesc<NCH>& d, uint4 raw, uint4 pw) {
 // same branches through decode_header (weight range, partition count and
 // colour range, up to collisions of the fold), so sorting a chunk's blocks by
 // class before the header stage keeps the lanes of a wave on one path. Constant blocks (void
-// extent, reserved or invalid modes) are class kPathKeys - 1.
+// extent, reserved or invalid modes, too few colour bits: the blocks
+// decode_header makes constant, by the same tests) are class kPathKeys - 1,
+// and only they are; block_part_words relies on that.
 constexpr int kPathKeys = 64;
 
 __device__ inline int block_path_key(uint4 raw, const LdsTables& L) {
@@ -540,14 +562,22 @@ __device__ inline int block_path_key(uint4 raw, const LdsTables& L) {
     return ((int(akv::mode_range(md)) * 4 + parts - 1) * 17 + crange - akv::kRange6) % (kPathKeys - 1);
 }
 
-// The partition-pattern words a block selects (any 128-bit value selects an
-// in-range entry; blocks with one partition, void-extent and error blocks
-// ignore it). This is the header stage's only global-memory read, so callers
-// issue it early, ahead of other loads.
+// The partition-pattern table entry a block's bits select (any 128-bit value
+// selects an in-range entry; which blocks use it, block_part_words decides).
+// A plain load, so that callers can issue it early and use it late.
 __device__ inline uint4 partition_words(uint4 raw, const AkvTables* __restrict__ tab) {
     const int parts = int((raw.x >> 11) & 3) + 1;
-    if (parts == 1) return uint4{0, 0, 0, 0};
-    return *reinterpret_cast<const uint4*>(tab->partition[parts - 2][(raw.x >> 13) & 0x3FF]);
+    return *reinterpret_cast<const uint4*>(tab->partition[max(parts - 2, 0)][(raw.x >> 13) & 0x3FF]);
+}
+
+// BlockDesc::part of a block: its pattern words, or zero for one partition and
+// for the blocks decode_header turns into a constant colour (void extent,
+// reserved modes, too few colour bits: exactly block_path_key ==
+// kPathKeys - 1), whose one table entry is entry 0.
+__device__ inline uint4 block_part_words(uint4 raw, uint4 words, int key) {
+    const bool zero = ((raw.x >> 11) & 3) == 0 || key == kPathKeys - 1;
+    const uint32_t m = zero ? 0u : ~0u;
+    return uint4{words.x & m, words.y & m, words.z & m, words.w & m};
 }
 
 // Stage 1: one lane decodes the block stashed in `d` (stash_block) into `d`.
@@ -615,8 +645,6 @@ __device__ __attribute__((always_inline)) inline void decode_header(const LdsTab
         set_constant(d, 0xFFFF, 0, 0xFFFF, 0xFFFF);
         return;
     }
-    const uint4 pw = *reinterpret_cast<const uint4*>(d.tab + 4);
-
     // Colour integer sequence -> unquantised colour bytes.
     decode_colour_values(blk, color_start, crange, 2 * pairs, L, cv);
 
@@ -662,10 +690,6 @@ __device__ __attribute__((always_inline)) inline void decode_header(const LdsTab
             for (int ch = 0; ch < NCH; ++ch) d.ep[p][ch] = ep[ch];
         }
     }
-    d.part[0] = pw.x;
-    d.part[1] = pw.y;
-    d.part[2] = pw.z;
-    d.part[3] = pw.w;
     d.info = (md & 0xFFu) | (dual ? kInfoDual : 0u) | (ccs << 9) | (uint32_t(nb) << kInfoNbShift) |
              (uint32_t(wrange) << kInfoRangeShift) | (uint32_t(levels) << kInfoLevelsShift) |
              (identity ? kInfoIdentity : 0u) | (table ? kInfoTable : 0u);

@@ -82,23 +82,43 @@ struct Grp {
 // Q as the B operand of the block-diagonal S^T = K.Q^T, split into fp16 high
 // and low parts, kept in LDS (the same for every wave): qs[2 * ks + part][lane]
 // for lane (column r, g) holds head r % Gs, dims 32*(ks/2) + 8*g + 4*(ks%2) + j
-// (j = 0..3), matching the K row loads. Written by the first wave.
+// (j = 0..3), matching the K row loads. Loaded and stored by the first wave,
+// in two halves so that a kernel can issue the loads early: `qrow` is 16-byte
+// aligned, every load is unconditional (slots h >= G read head G - 1 and are
+// zeroed).
+template <int D, int G>
+struct QStage {
+    float4 x[D / 16];
+    __device__ void load(const float* __restrict__ qrow) {
+        const int lane = threadIdx.x & 63, h = (lane & 15) % Grp<G, D>::Gs, g = lane >> 4;
+        const float* src = qrow + size_t(min(h, G - 1)) * D + 8 * g;
+#pragma unroll
+        for (int ks = 0; ks < D / 16; ++ks)
+            x[ks] = *reinterpret_cast<const float4*>(src + 32 * (ks / 2) + 4 * (ks % 2));
+    }
+    __device__ void store(float qscale, uint2* qs) const {
+        const int lane = threadIdx.x & 63, h = (lane & 15) % Grp<G, D>::Gs;
+#pragma unroll
+        for (int ks = 0; ks < D / 16; ++ks) {
+            const float e[4] = {x[ks].x, x[ks].y, x[ks].z, x[ks].w};
+            half4 hi, lo;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float v = h < G ? e[j] * qscale : 0.0f;
+                hi[j] = _Float16(v);
+                lo[j] = _Float16(v - float(hi[j]));
+            }
+            qs[(2 * ks) * 64 + lane] = __builtin_bit_cast(uint2, hi);
+            qs[(2 * ks + 1) * 64 + lane] = __builtin_bit_cast(uint2, lo);
+        }
+    }
+};
+
 template <int D, int G>
 __device__ inline void store_q(const float* __restrict__ qrow, float qscale, uint2* qs) {
-    const int lane = threadIdx.x & 63, n16 = lane & 15, g = lane >> 4;
-    const int h = n16 % Grp<G, D>::Gs;
-#pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
-        half4 hi, lo;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float v = h < G ? qrow[size_t(h) * D + 32 * (ks / 2) + 8 * g + 4 * (ks % 2) + j] * qscale : 0.0f;
-            hi[j] = _Float16(v);
-            lo[j] = _Float16(v - float(hi[j]));
-        }
-        qs[(2 * ks) * 64 + lane] = __builtin_bit_cast(uint2, hi);
-        qs[(2 * ks + 1) * 64 + lane] = __builtin_bit_cast(uint2, lo);
-    }
+    QStage<D, G> st;
+    st.load(qrow);
+    st.store(qscale, qs);
 }
 
 __device__ inline half4 masked(uint2 v, uint32_t m) { return __builtin_bit_cast(half4, uint2{v.x & m, v.y & m}); }
@@ -502,7 +522,9 @@ struct AstcShared {
 
 // The chunk's blocks (one per lane).
 __device__ inline uint4 load_block(const uint4* __restrict__ bseq, uint32_t cols, int row0, int nblk, int tid) {
-    return tid < nblk ? bseq[size_t(row0) * cols + tid] : uint4{0, 0, 0, 0};
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(seq_rsrc(bseq + size_t(row0) * cols, uint32_t(nblk) * 16),
+                                                         16 * tid, 0, 0);   // lanes past nblk read zero
+    return uint4{v[0], v[1], v[2], v[3]};
 }
 
 // Texels of one 16-token tile straight into the P.V operand: lane (n16, g)

@@ -66,13 +66,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
     const uint16_t* oseq = DUMP ? nullptr : voffset + seq_kv * p.tokens;
 
     auto chunk_blocks = [&](int c0) { return int((min(CT, split_end - c0) + by - 1) / by * cols); };
-    uint4 raw = load_block(bseq, cols, split_begin / by, chunk_blocks(split_begin), tid);
-    uint4 pw = tid < chunk_blocks(split_begin) ? partition_words(raw, tab) : uint4{0, 0, 0, 0};
-    stage_tables(tab, sh.tabs, tid, kThreads);
-    if (tid < kPathKeys) sh.key_count[tid] = 0;
-
+    auto k_rsrc = [&](int c0) {
+        return seq_rsrc(DUMP ? nullptr : kseq + size_t(c0) * D, DUMP ? 0u : uint32_t(min(CT, split_end - c0)) * D * 2);
+    };
+    // Prologue: the decode tables and Q (from L2) and the first chunk's
+    // blocks, all issued before the first wait.
+    TableStage<kThreads> tables;
+    tables.load(tab, tid);
+    QStage<D, G> qst;
     if constexpr (!DUMP)
-        if (wave == 0) store_q<D, G>(q + (size_t(b) * p.query_heads + size_t(kh) * G) * D, a.qscale, &sh.q[0][0]);
+        if (wave == 0) qst.load(q + (size_t(b) * p.query_heads + size_t(kh) * G) * D);
+    uint4 raw = load_block(bseq, cols, split_begin / by, chunk_blocks(split_begin), tid);
+    tables.store(sh.tabs, tid);
+    if constexpr (!DUMP)
+        if (wave == 0) qst.store(a.qscale, &sh.q[0][0]);
+    if (tid < kPathKeys) sh.key_count[tid] = 0;
 
     // This lane's texel columns: x = n16 + 16 * kc -> block column and x in block.
     int bcol[C::kColGroups], xin[C::kColGroups];
@@ -94,43 +102,41 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
         const int ntok = min(CT, split_end - c0);
         const int ntiles = (ntok + 15) >> 4;
         const int nblk = chunk_blocks(c0);
-        // 1. Loads (the chunk's blocks and their partition-pattern words were
-        // requested during the previous chunk): the first K tiles of this
-        // wave's first group, per-token scale/offset, the next chunk's blocks.
-        uint4 kreg[TPG * C::kRowLoads];
-        const __amdgpu_buffer_rsrc_t krs = seq_rsrc(DUMP ? nullptr : kseq + size_t(c0) * D, DUMP ? 0u : uint32_t(ntok) * D * 2);
-        if constexpr (!DUMP) {
-#pragma unroll
-            for (int t = 0; t < kKEarly; ++t)
-                load_k_tile<D>(kreg + t * C::kRowLoads, krs, 16 * (TPG * wave + t), lane);
-        }
-        // Per-token V scale | offset << 16 for up to two tokens per lane.
+        // 1. Loads. Only the blocks cross chunks (requested one chunk ahead:
+        // the header stage needs them first). The rest is requested here and
+        // first used after the header stage, which covers its latency: the
+        // blocks' partition-pattern words (they depend on the blocks), the
+        // per-token scale/offset (two tokens per lane, clamped index), the
+        // first K tiles of this wave's first group. Memory waits count loads
+        // in issue order, so they are issued in the order of first use.
+        const uint4 raw_now = raw;
+        const uint4 pat = partition_words(raw_now, tab);
+        uint32_t sc[2] = {0, 0}, of[2] = {0, 0};
         static_assert(C::kMaxTok <= 2 * kThreads, "two scale/offset tokens per lane");
-        uint32_t so[2] = {0, 0};
         if constexpr (!DUMP) {
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                const int t = tid + i * kThreads;
-                if (t < ntok) so[i] = uint32_t(sseq[c0 + t]) | (uint32_t(oseq[c0 + t]) << 16);
+                const int tc = c0 + min(tid + i * kThreads, ntok - 1);
+                sc[i] = sseq[tc];
+                of[i] = oseq[tc];
             }
         }
-        const uint4 raw_now = raw;
         if (c0 + CT < split_end) raw = load_block(bseq, cols, (c0 + CT) / by, chunk_blocks(c0 + CT), tid);
+        uint4 kreg[TPG * C::kRowLoads];
+        const __amdgpu_buffer_rsrc_t krs = k_rsrc(c0);
+        if constexpr (!DUMP) {
+#pragma unroll
+            for (int t = 0; t < kKEarly; ++t) load_k_tile<D>(kreg + t * C::kRowLoads, krs, 16 * (TPG * wave + t), lane);
+        }
         // 2. Block headers, with the chunk's blocks sorted by decode-path class
         // so that the lanes of a wave take the same branches. Each block's raw
-        // bits and pattern words wait in its own descriptor slot; the lane that
-        // decodes a block reads them from there and overwrites that slot.
+        // bits wait in its own descriptor slot; the lane that decodes a block
+        // reads them from there and overwrites that slot.
         int key = 0, rank = 0;
         if (tid < nblk) {
             key = block_path_key(raw_now, sh.tabs);
-            stash_block(sh.u.h.desc[tid], raw_now, pw);
+            stash_block(sh.u.h.desc[tid], raw_now);
             rank = int(atomicAdd(&sh.key_count[key], 1u));
-        }
-        // Tokens past the chunk up to the tile edge get scale = offset = 0.
-        if constexpr (!DUMP) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                if (tid + i * kThreads < 16 * ntiles) sh.so[tid + i * kThreads] = so[i];
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -152,8 +158,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
         if (tid < nblk) sh.order[sh.key_base[key] + rank] = uint8_t(tid);
         __syncthreads();
         if (tid < nblk) decode_header<NCH>(sh.tabs, sh.u.h.desc[sh.order[tid]], sh.u.h.cv[tid]);
-        // The next chunk's pattern words (its blocks have arrived by now).
-        if (c0 + CT < split_end) pw = tid < chunk_blocks(c0 + CT) ? partition_words(raw, tab) : uint4{0, 0, 0, 0};
+        // What the texel stage needs besides the headers: each lane's own
+        // block's partition words, and the per-token scale | offset << 16
+        // (zero past the chunk, up to the tile edge).
+        if (tid < nblk) {
+            const uint4 w = block_part_words(raw_now, pat, key);
+            uint32_t* part = sh.u.h.desc[tid].part;   // 4-byte aligned
+            part[0] = w.x;
+            part[1] = w.y;
+            part[2] = w.z;
+            part[3] = w.w;
+        }
+        if constexpr (!DUMP) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int t = tid + i * kThreads;
+                if (t < 16 * ntiles) sh.so[t] = t < ntok ? sc[i] | (of[i] << 16) : 0u;
+            }
+        }
         __syncthreads();
         // 3. This wave's groups of TPG consecutive tiles (every fourth group):
         // S for the whole group, then for each tile its texels straight into
@@ -364,12 +386,18 @@ __global__ __launch_bounds__(kThreads) void decode_blocks_kernel(const uint4* __
     const size_t first = size_t(blockIdx.x) * kThreads;
     const int nblk = int(min(size_t(kThreads), n - first));
     const uint4 raw = tid < nblk ? blocks[first + tid] : uint4{0, 0, 0, 0};
-    const uint4 pw = tid < nblk ? partition_words(raw, tab) : uint4{0, 0, 0, 0};
-    stage_tables(tab, sh.tabs, tid, kThreads);
+    const uint4 pw = partition_words(raw, tab);
+    stage_tables<kThreads>(tab, sh.tabs, tid);
     __syncthreads();
     if (tid < nblk) {
-        stash_block(sh.desc[tid], raw, pw);
+        stash_block(sh.desc[tid], raw);
         decode_header<4>(sh.tabs, sh.desc[tid], sh.cv[tid]);
+        const uint4 w = block_part_words(raw, pw, block_path_key(raw, sh.tabs));
+        uint32_t* part = sh.desc[tid].part;
+        part[0] = w.x;
+        part[1] = w.y;
+        part[2] = w.z;
+        part[3] = w.w;
     }
     __syncthreads();
     for (int it = tid; it < nblk * f.ntex; it += kThreads) {

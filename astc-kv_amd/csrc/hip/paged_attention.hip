@@ -114,12 +114,17 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
         return vpool[((size_t(pid) * Hkv + kh) * rpp + prow) * cols + col];
     };
 
+    // Prologue: the decode tables and Q (from L2), the split's page ids and
+    // the first chunk's blocks, all issued before the first wait.
+    TableStage<kThreads> tables;
+    tables.load(tab, tid);
+    QStage<D, G> qst;
+    if (wave == 0) qst.load(q + (size_t(b) * p.query_heads + size_t(kh) * G) * D);
     uint4 raw = load_blk(split_begin, chunk_blocks(split_begin), true);
-    uint4 pw = tid < chunk_blocks(split_begin) ? partition_words(raw, tab) : uint4{0, 0, 0, 0};
     if (tid < npages) shp.pages[tid] = seq_table[tid];
-    stage_tables(tab, sh.tabs, tid, kThreads);
+    tables.store(sh.tabs, tid);
+    if (wave == 0) qst.store(a.qscale, &sh.q[0][0]);
     if (tid < kPathKeys) sh.key_count[tid] = 0;
-    if (wave == 0) store_q<D, G>(q + (size_t(b) * p.query_heads + size_t(kh) * G) * D, a.qscale, &sh.q[0][0]);
 
     int bcol[C::kColGroups], xin[C::kColGroups];
 #pragma unroll
@@ -168,39 +173,37 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
         const int ntiles = (ntok + 15) >> 4;
         const int nastc = chunk_astc(c0);
         const int nblk = chunk_blocks(c0);
-        // 1. Loads: the first K tiles of this wave's first group, per-token
-        // scale/offset (tail tokens: 1 and 0), the next chunk's blocks.
-#pragma unroll
-        for (int t = 0; t < kKEarly; ++t) load_k(kw + t * kKWords, c0, 16 * (TPG * wave + t));
+        // 1. Loads. Only the blocks cross chunks (requested one chunk ahead:
+        // the header stage needs them first). The rest is requested here and
+        // first used after the header stage, which covers its latency: the
+        // blocks' partition-pattern words, the per-token scale/offset (two
+        // tokens per lane; every token of the split has a page, so a clamped
+        // index reads in bounds), the first K tiles of this wave's first
+        // group. Memory waits count loads in issue order, so they are issued
+        // in the order of first use.
+        const uint4 raw_now = raw;
+        const uint4 pat = partition_words(raw_now, tab);
         static_assert(C::kMaxTok <= 2 * kThreads, "two scale/offset tokens per lane");
-        uint32_t so[2] = {0, 0};
+        uint32_t sc[2], of[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const int t = tid + i * kThreads;
-            if (t < ntok) {
-                if (c0 + t < full) {
-                    int pid, pos;
-                    page_of(c0 + t, pid, pos);
-                    const size_t at = (size_t(pid) * Hkv + kh) * P + pos;
-                    so[i] = uint32_t(vscale[at]) | (uint32_t(voffset[at]) << 16);
-                } else {
-                    so[i] = 0x3C00u;   // fp16 1.0, offset 0
-                }
-            }
+            int pid, pos;
+            page_of(c0 + min(tid + i * kThreads, ntok - 1), pid, pos);
+            const size_t at = (size_t(pid) * Hkv + kh) * P + pos;
+            sc[i] = vscale[at];
+            of[i] = voffset[at];
         }
-        const uint4 raw_now = raw;
         if (c0 + CT < split_end) raw = load_blk(c0 + CT, chunk_blocks(c0 + CT), false);
+#pragma unroll
+        for (int t = 0; t < kKEarly; ++t) load_k(kw + t * kKWords, c0, 16 * (TPG * wave + t));
         // 2. Block headers (the blocks of the chunk's ASTC tokens), sorted by
         // decode-path class.
         int key = 0, rank = 0;
         if (tid < nblk) {
             key = block_path_key(raw_now, sh.tabs);
-            stash_block(sh.u.h.desc[tid], raw_now, pw);
+            stash_block(sh.u.h.desc[tid], raw_now);
             rank = int(atomicAdd(&sh.key_count[key], 1u));
         }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-            if (tid + i * kThreads < 16 * ntiles) sh.so[tid + i * kThreads] = so[i];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
             if (tid + i * kThreads < C::kMaxTok)
@@ -222,8 +225,22 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
         if (tid < nblk) sh.order[sh.key_base[key] + rank] = uint8_t(tid);
         __syncthreads();
         if (tid < nblk) decode_header<NCH>(sh.tabs, sh.u.h.desc[sh.order[tid]], sh.u.h.cv[tid]);
-        if (c0 + CT < split_end)
-            pw = tid < chunk_blocks(c0 + CT) ? partition_words(raw, tab) : uint4{0, 0, 0, 0};
+        // Each lane's own block's partition words, and the per-token scale |
+        // offset << 16 (tail tokens: fp16 1.0 and 0; zero past the chunk, up
+        // to the tile edge).
+        if (tid < nblk) {
+            const uint4 w = block_part_words(raw_now, pat, key);
+            uint32_t* part = sh.u.h.desc[tid].part;   // 4-byte aligned
+            part[0] = w.x;
+            part[1] = w.y;
+            part[2] = w.z;
+            part[3] = w.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int t = tid + i * kThreads;
+            if (t < 16 * ntiles) sh.so[t] = t >= ntok ? 0u : c0 + t < full ? sc[i] | (of[i] << 16) : 0x3C00u;
+        }
         __syncthreads();
         // 3. Tile groups; tiles at or past `full` read V from the FP16 tail.
 #pragma unroll
