@@ -602,6 +602,7 @@ int run_astc(const AkvAttnParams* p, const float* q, const uint16_t* k, const vo
     if (int rc = check_astc(p)) return rc;
     if (!q || !k || !v_blocks || !v_scale || !v_offset || !partial || !stats || (with_merge && !out))
         return AKV_HIP_ERR_NULL;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v_blocks)) return AKV_HIP_ERR_ALIGN;
     const AkvTables* tab = nullptr;
     if (int rc = device_tables(int(p->block_x), int(p->block_y), &tab)) return rc;
     KernelArgs a;
@@ -656,6 +657,7 @@ int akv_hip_fp16_attention_fused(const AkvAttnParams* p, const float* q, const u
     uint32_t G = 0;
     if (int rc = check_common(p, &G)) return rc;
     if (!q || !k || !v || !partial || !stats || !out) return AKV_HIP_ERR_NULL;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v)) return AKV_HIP_ERR_ALIGN;
     KernelArgs a;
     if (int rc = make_args(p, false, &a)) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -677,6 +679,7 @@ int akv_hip_decode_values(const AkvAttnParams* p, const void* v_blocks, uint16_t
     if (int rc = check_common(p, &G)) return rc;
     if (int rc = check_astc(p)) return rc;
     if (!v_blocks || !u) return AKV_HIP_ERR_NULL;
+    if (!aligned16(v_blocks)) return AKV_HIP_ERR_ALIGN;
     const AkvTables* tab = nullptr;
     if (int rc = device_tables(int(p->block_x), int(p->block_y), &tab)) return rc;
     KernelArgs a;
@@ -688,6 +691,7 @@ int akv_hip_decode_values(const AkvAttnParams* p, const void* v_blocks, uint16_t
 
 int akv_hip_decode_blocks(const void* blocks, size_t n, unsigned bx, unsigned by, uint16_t* texels, void* stream) {
     if ((!blocks || !texels) && n) return AKV_HIP_ERR_NULL;
+    if (n && !aligned16(blocks)) return AKV_HIP_ERR_ALIGN;
     if (bx < 4 || by < 4 || bx > 12 || by > 12 || bx * by > unsigned(akv::kMaxTexels)) return AKV_HIP_ERR_FOOTPRINT;
     if (n == 0) return 0;
     const AkvTables* tab = nullptr;
@@ -718,6 +722,7 @@ const char* akv_hip_error_string(int code) {
         case AKV_HIP_ERR_FOOTPRINT: return "unsupported ASTC footprint";
         case AKV_HIP_ERR_TILE: return "tile_tokens/splits inconsistent (tile must be a positive multiple of "
                                       "block_y and splits = ceil(tokens/tile))";
+        case AKV_HIP_ERR_ALIGN: return "q, k, v and the V blocks must be 16-byte aligned";
         default: return code > 0 ? hipGetErrorString(hipError_t(code)) : "unknown error";
     }
 }

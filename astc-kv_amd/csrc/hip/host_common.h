@@ -20,4 +20,7 @@ Footprint footprint(uint32_t bx, uint32_t by);
 
 inline int as_int(hipError_t e) { return e == hipSuccess ? 0 : int(e); }
 
+// The kernels read Q, K, V and the V blocks with 16-byte vector loads.
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 }  // namespace akv_hip

@@ -414,6 +414,8 @@ int akv_hip_paged_decode_attention(const AkvPagedParams* p, const float* q, cons
     if (!q || !k_pages || !v_blocks || !v_scale || !v_offset || !block_table || !seq_lens || !partial || !stats ||
         !out || !arrivals || (p->k_format == AKV_K_U4G32 && !k_meta))
         return AKV_HIP_ERR_NULL;
+    if (!aligned16(q) || !aligned16(k_pages) || !aligned16(v_blocks) || (v_tail && !aligned16(v_tail)))
+        return AKV_HIP_ERR_ALIGN;
     const AkvTables* tab = nullptr;
     if (int rc = device_tables(int(p->block_x), int(p->block_y), &tab)) return rc;
     PagedArgs a;

@@ -21,7 +21,8 @@
  *   akv_hip_decode_blocks     standalone block decode to FP16 RGBA texels
  *                             (decode_texture, :257-269)
  *
- * Conventions: every pointer is a device pointer owned by the caller; `stream`
+ * Conventions: every pointer is a device pointer owned by the caller; q, k, v
+ * and the V blocks (and the paged pools) are 16-byte aligned; `stream`
  * is a hipStream_t (NULL = default stream); calls are stream-ordered and never
  * synchronise the host, except the first call for a footprint on a device,
  * which uploads that footprint's decode tables (a blocking copy). Return 0 on
@@ -57,7 +58,8 @@ enum {
     AKV_HIP_ERR_NULL = -1,        /* a required pointer is NULL */
     AKV_HIP_ERR_SHAPE = -2,       /* unsupported or inconsistent shape */
     AKV_HIP_ERR_FOOTPRINT = -3,   /* unsupported ASTC footprint */
-    AKV_HIP_ERR_TILE = -4         /* tile_tokens/splits inconsistent */
+    AKV_HIP_ERR_TILE = -4,        /* tile_tokens/splits inconsistent */
+    AKV_HIP_ERR_ALIGN = -5        /* q, k, v or the V blocks not 16-byte aligned */
 };
 
 enum { AKV_LAYOUT_SCALAR = 0, AKV_LAYOUT_RGBA = 1 };

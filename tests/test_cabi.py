@@ -90,6 +90,20 @@ def test_rejected_parameters(hip, kw, code):
     assert hip.akv_hip_error_string(code).decode() != "unknown error"
 
 
+@pytest.mark.parametrize("bad", ["q", "k", "v"])
+def test_misaligned_pointers_rejected_before_any_launch(hip, bad):
+    # Fake device addresses: the argument checks return before anything is
+    # dereferenced or launched, so this runs without a GPU.
+    fn = hip.akv_hip_decode_attention
+    fn.argtypes = [ct.POINTER(Params)] + [ct.c_void_p] * 9
+    fn.restype = ct.c_int
+    ptr = {"q": 0x10000, "k": 0x20000, "v": 0x30000}
+    ptr[bad] += 4
+    args = [ptr["q"], ptr["k"], ptr["v"], 0x40000, 0x50000, 0x60000, 0x70000, 0x80000, None]
+    assert fn(ct.byref(c3(tile_tokens=515, splits=16)), *args) == -5
+    assert b"16-byte" in hip.akv_hip_error_string(-5)
+
+
 def test_null_params_and_error_strings(hip):
     assert hip.akv_hip_task_tokens(None, 1) == -1
     assert hip.akv_hip_error_string(0) == b"success"
