@@ -156,6 +156,34 @@ __device__ inline uint32_t opaque_mask(bool c) {
     return m;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave, without LDS: DPP row
+// shifts (1, 2, 4, 8; lanes shifted in from outside the 16-lane row read 0)
+// scan each row, then each row adds the totals of the rows before it (read
+// with readlane).
+__device__ inline uint32_t wave_inclusive_scan(uint32_t v) {
+    v += uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x111, 0xF, 0xF, false));   // row_shr:1
+    v += uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x112, 0xF, 0xF, false));   // row_shr:2
+    v += uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x114, 0xF, 0xF, false));   // row_shr:4
+    v += uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x118, 0xF, 0xF, false));   // row_shr:8
+    const uint32_t r0 = uint32_t(__builtin_amdgcn_readlane(int(v), 15));
+    const uint32_t r1 = uint32_t(__builtin_amdgcn_readlane(int(v), 31));
+    const uint32_t r2 = uint32_t(__builtin_amdgcn_readlane(int(v), 47));
+    const int row = int(threadIdx.x & 63) >> 4;
+    return v + (row >= 1 ? r0 : 0u) + (row >= 2 ? r1 : 0u) + (row >= 3 ? r2 : 0u);
+}
+
+// Second half of the counting sort of a chunk's blocks by decode-path class
+// (after the class counts are complete): every wave scans the 64 counts
+// itself and writes the sorted positions of its own blocks; the base of a
+// lane's class comes from the scanning lane of that class.
+__device__ inline void place_by_class(const uint32_t* key_count, uint8_t* order, int key, int rank, bool mine,
+                                      int tid) {
+    const uint32_t c = key_count[tid & 63];
+    const uint32_t excl = wave_inclusive_scan(c) - c;
+    const uint32_t base = uint32_t(__shfl(int(excl), key, 64));
+    if (mine) order[base + uint32_t(rank)] = uint8_t(tid);
+}
+
 // Buffer resource over `bytes` bytes from `base` (raw, stride 0): loads past
 // the end return zero without touching memory.
 __device__ inline __amdgpu_buffer_rsrc_t seq_rsrc(const void* base, uint32_t bytes) {
@@ -514,7 +542,6 @@ struct AstcShared {
     uint32_t so[C::kMaxTok];                 // per-token V scale | offset << 16 (fp16)
     uint32_t tokrow[C::kMaxTok];             // token_row_entry of each chunk token
     uint32_t key_count[kPathKeys];           // blocks per decode-path class (zero between chunks)
-    uint32_t key_base[kPathKeys];            // first sorted position of each class
     uint8_t order[C::kMaxBlocks];            // blocks sorted by decode-path class
     uint2 q[2 * C::kKSteps][64];             // Q operands (fp16 high, low)
     WaveStats ws;

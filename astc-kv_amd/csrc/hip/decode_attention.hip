@@ -142,21 +142,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
         for (int i = 0; i < 2; ++i)
             if (tid + i * kThreads < C::kMaxTok)
                 sh.tokrow[tid + i * kThreads] = token_row_entry(tid + i * kThreads, ntok, a.mag_by, f, cols);
-        __syncthreads();
-        if (wave == 0) {   // exclusive scan of the class counts (kPathKeys == 64 lanes)
-            const uint32_t c = sh.key_count[lane];
-            uint32_t incl = c;
-#pragma unroll
-            for (int d = 1; d < 64; d <<= 1) {
-                const uint32_t t = __shfl_up(incl, d, 64);
-                if (lane >= d) incl += t;
-            }
-            sh.key_base[lane] = incl - c;
-            sh.key_count[lane] = 0;
-        }
-        __syncthreads();
-        if (tid < nblk) sh.order[sh.key_base[key] + rank] = uint8_t(tid);
-        __syncthreads();
+        __syncthreads();   // class counts complete
+        static_assert(kPathKeys == 64, "one class per lane");
+        place_by_class(sh.key_count, sh.order, key, rank, tid < nblk, tid);
+        __syncthreads();   // sorted order complete (and every count read)
+        if (wave == 0) sh.key_count[lane] = 0;   // for the next chunk (two barriers away)
         if (tid < nblk) decode_header<NCH>(sh.tabs, sh.u.h.desc[sh.order[tid]], sh.u.h.cv[tid]);
         // What the texel stage needs besides the headers: each lane's own
         // block's partition words, and the per-token scale | offset << 16

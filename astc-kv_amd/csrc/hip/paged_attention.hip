@@ -209,21 +209,11 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
             if (tid + i * kThreads < C::kMaxTok)
                 sh.tokrow[tid + i * kThreads] =
                     token_row_entry(tid + i * kThreads, max(nastc, 1), a.mag_by, f, uint32_t(cols));
-        __syncthreads();
-        if (wave == 0) {   // exclusive scan of the class counts (kPathKeys == 64 lanes)
-            const uint32_t c = sh.key_count[lane];
-            uint32_t incl = c;
-#pragma unroll
-            for (int d = 1; d < 64; d <<= 1) {
-                const uint32_t t = __shfl_up(incl, d, 64);
-                if (lane >= d) incl += t;
-            }
-            sh.key_base[lane] = incl - c;
-            sh.key_count[lane] = 0;
-        }
-        __syncthreads();
-        if (tid < nblk) sh.order[sh.key_base[key] + rank] = uint8_t(tid);
-        __syncthreads();
+        __syncthreads();   // class counts complete
+        static_assert(kPathKeys == 64, "one class per lane");
+        place_by_class(sh.key_count, sh.order, key, rank, tid < nblk, tid);
+        __syncthreads();   // sorted order complete (and every count read)
+        if (wave == 0) sh.key_count[lane] = 0;   // for the next chunk (two barriers away)
         if (tid < nblk) decode_header<NCH>(sh.tabs, sh.u.h.desc[sh.order[tid]], sh.u.h.cv[tid]);
         // Each lane's own block's partition words, and the per-token scale |
         // offset << 16 (tail tokens: fp16 1.0 and 0; zero past the chunk, up
