@@ -63,12 +63,15 @@ def lib():
         L.akv_hip_paged_decode_attention.argtypes = [PP] + [vp] * 14
         L.akv_hip_paged_task_tokens.argtypes = [PP]
         L.akv_hip_paged_task_tokens.restype = ct.c_int
+        L.akv_hip_paged_append.argtypes = [PP] + [vp] * 8
+        L.akv_hip_paged_commit_pages.argtypes = [PP, ct.c_uint32] + [vp] * 8
         L.akv_hip_task_tokens.argtypes = [P, ct.c_int]
         L.akv_hip_task_tokens.restype = ct.c_int
         L.akv_hip_error_string.argtypes = [ct.c_int]
         L.akv_hip_error_string.restype = ct.c_char_p
         for f in ("akv_hip_decode_attention", "akv_hip_attention_split", "akv_hip_attention_merge",
-                  "akv_hip_fp16_attention", "akv_hip_decode_values", "akv_hip_decode_blocks"):
+                  "akv_hip_fp16_attention", "akv_hip_decode_values", "akv_hip_decode_blocks",
+                  "akv_hip_paged_decode_attention", "akv_hip_paged_append", "akv_hip_paged_commit_pages"):
             getattr(L, f).restype = ct.c_int
         _LIB = L
     return _LIB
@@ -347,6 +350,7 @@ class DevicePagedKV:
     block_y: int
     page_tokens: int
     k_format: str
+    table_host: np.ndarray | None = None   # host copy of block_table (page ids for append/commit)
 
     @classmethod
     def from_host(cls, pk, device="cuda") -> "DevicePagedKV":
@@ -354,7 +358,7 @@ class DevicePagedKV:
             return None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(device)
         return cls(dev(pk.k_pages), dev(pk.k_meta), dev(pk.v_blocks), dev(pk.v_scale), dev(pk.v_offset),
                    dev(pk.block_table), dev(pk.seq_lens), dev(pk.v_tail), pk.seq_lens.tolist(), pk.dim, pk.layout,
-                   pk.block_x, pk.block_y, pk.page_tokens, pk.k_format)
+                   pk.block_x, pk.block_y, pk.page_tokens, pk.k_format, np.array(pk.block_table))
 
     @property
     def batch(self) -> int:
@@ -363,6 +367,52 @@ class DevicePagedKV:
     @property
     def kv_heads(self) -> int:
         return self.k_pages.shape[1]
+
+    def pool_params(self) -> AkvPagedParams:
+        """The pool fields of AkvPagedParams (append and commit use no others)."""
+        return AkvPagedParams(self.batch, max(self.lens), self.kv_heads, self.kv_heads, self.dim, self.page_tokens,
+                              self.block_table.shape[1], self.k_pages.shape[0], 0, 0, LAYOUTS[self.layout],
+                              self.block_x, self.block_y, self.v_blocks.shape[3], K_FORMATS[self.k_format])
+
+    def append(self, k_new: torch.Tensor, v_new: torch.Tensor, quality: float = 50, threads: int | None = None):
+        """Append one token per sequence (k_new, v_new f32 [B, Hkv, D] on the
+        GPU) with akv_hip_paged_append and advance the lengths. Each page this
+        completes is encoded on the host from its FP16 tail (astc_kv.atlas, the
+        encoder build_paged uses) and copied into its V pool page with one
+        akv_hip_paged_commit_pages launch. Returns the sequences whose page
+        completed."""
+        if self.v_tail is None:
+            raise ValueError("appending needs the FP16 tail (build_paged(tail=True))")
+        shape = (self.batch, self.kv_heads, self.dim)
+        _need(k_new, torch.float32, "k_new", shape)
+        _need(v_new, torch.float32, "v_new", shape)
+        P = self.page_tokens
+        for i, n in enumerate(self.lens):
+            pg = n // P
+            if pg >= self.table_host.shape[1] or not 0 <= int(self.table_host[i, pg]) < self.k_pages.shape[0]:
+                raise ValueError(f"sequence {i} has no page for token {n} (reserve pages in build_paged)")
+        params = self.pool_params()
+        dev = k_new.device
+        _check(lib().akv_hip_paged_append(ct.byref(params), _ptr(k_new), _ptr(v_new), _ptr(self.k_pages),
+                                          _ptr(self.k_meta), _ptr(self.block_table), _ptr(self.seq_lens),
+                                          _ptr(self.v_tail), _stream(dev)))
+        self.seq_lens += 1
+        self.lens = [n + 1 for n in self.lens]
+        done = [i for i, n in enumerate(self.lens) if n % P == 0]
+        if done:
+            from .atlas import build_atlas
+            tails = self.v_tail[done].float().cpu().numpy()          # [n, Hkv, P, D]
+            at = build_atlas(tails, self.layout, (self.block_x, self.block_y), P, quality, threads)
+            ids = torch.tensor([int(self.table_host[i, self.lens[i] // P - 1]) for i in done], dtype=torch.int32,
+                               device=dev)
+            blocks = torch.from_numpy(np.ascontiguousarray(at.blocks)).to(dev)
+            scale = torch.from_numpy(np.ascontiguousarray(at.scale)).to(dev)
+            offset = torch.from_numpy(np.ascontiguousarray(at.offset)).to(dev)
+            _check(lib().akv_hip_paged_commit_pages(ct.byref(params), len(done), _ptr(ids), _ptr(blocks), _ptr(scale),
+                                                    _ptr(offset), _ptr(self.v_blocks), _ptr(self.v_scale),
+                                                    _ptr(self.v_offset), _stream(dev)))
+            torch.cuda.current_stream(dev).synchronize()   # staging buffers are freed on return
+        return done
 
 
 def paged_params(cache: DevicePagedKV, query_heads: int, tile: int | None = None, cu_count: int = 256) -> AkvPagedParams:

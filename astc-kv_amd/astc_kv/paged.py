@@ -71,10 +71,11 @@ class PagedKV:
 
 def build_paged(k_seqs, v_seqs, layout: str = "scalar", block=(6, 6), page_tokens: int = 96,
                 quality: float = 50, k_format: str = "fp16", tail: bool = True, seed: int = 0,
-                threads: int | None = None, progress=None) -> PagedKV:
+                threads: int | None = None, progress=None, reserve_tokens: int = 0) -> PagedKV:
     """k_seqs, v_seqs: per sequence [Hkv, T_i, D] (K fp16 or float, V float).
-    Pages are assigned in a seeded random order. progress(i, n), if given, is
-    called after each sequence."""
+    Pages are assigned in a seeded random order; each sequence gets pages for
+    T_i + reserve_tokens tokens (the ones past T_i empty, for appends).
+    progress(i, n), if given, is called after each sequence."""
     bx, by = codec._footprint(block)
     if page_tokens % 16 or page_tokens % by:
         raise ValueError("page_tokens must be a multiple of 16 and of the block height")
@@ -89,7 +90,9 @@ def build_paged(k_seqs, v_seqs, layout: str = "scalar", block=(6, 6), page_token
     lens = [int(np.shape(v)[1]) for v in v_seqs]
     if min(lens) < 1:
         raise ValueError("empty sequence")
-    pages = [-(-t // P) for t in lens]
+    if reserve_tokens < 0:
+        raise ValueError("reserve_tokens must be >= 0")
+    pages = [-(-(t + reserve_tokens) // P) for t in lens]
     total = sum(pages)
     perm = np.random.default_rng(seed).permutation(total).astype(np.int32)
     rpp = P // by
@@ -121,7 +124,7 @@ def build_paged(k_seqs, v_seqs, layout: str = "scalar", block=(6, 6), page_token
             _, _, _, packed, off, sc = codec.affine_quantize_codes(k.astype(np.float32), 4, "token", 32)
             kk = packed.reshape(h, t, d // 2)
             meta = np.concatenate([off, sc], axis=-1).astype(np.float16)     # [h, t, d/32, 2]
-        for j, pid in enumerate(ids):
+        for j, pid in enumerate(ids[:-(-t // P)]):
             n = min(P, t - j * P)
             k_pages[pid, :, :n] = kk[:, j * P:j * P + n]
             if k_meta is not None:

@@ -18,6 +18,7 @@
 // format is a plan (docs/representation_v0.1.md:47-50, :84-95).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 #include "astc_decode_device.h"
@@ -278,16 +279,112 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
                         kWaves * D * kMaxG);
 }
 
+// --- append and page commit ----------------------------------------------------
+
+// fp16 bits of the largest float16 <= x and of the smallest float16 >= x (x
+// finite): round to nearest even, then one step toward -inf / +inf where that
+// rounded past x, as np.nextafter on float16 (from +-0 the step is to -+2^-24;
+// from -2^-24 up it is to -0).
+__device__ inline uint16_t fp16_floor_bits(float x) {
+    const _Float16 h = _Float16(x);
+    uint16_t b = __builtin_bit_cast(uint16_t, h);
+    if (float(h) > x) b = (b & 0x7FFF) == 0 ? uint16_t(0x8001) : (b & 0x8000) ? uint16_t(b + 1) : uint16_t(b - 1);
+    return b;
+}
+
+__device__ inline uint16_t fp16_ceil_bits(float x) {
+    const _Float16 h = _Float16(x);
+    uint16_t b = __builtin_bit_cast(uint16_t, h);
+    if (float(h) < x) b = (b & 0x7FFF) == 0 ? uint16_t(0x0001) : (b & 0x8000) ? uint16_t(b - 1) : uint16_t(b + 1);
+    return b;
+}
+
+__device__ inline float fp16_value(uint16_t b) { return float(__builtin_bit_cast(_Float16, b)); }
+
+// One new token per sequence into the pools, at row seq_len % P of page
+// block_table[b][seq_len / P]: K as fp16, or as 4-bit codes with the fp16
+// (offset, scale) of its group of 32 channels (affine_quantize(axis="token",
+// group=32), codec.py:218-250, all in fp32: o = fp16_floor(min), s =
+// fp16_ceil(max((max - o) / 15, 2^-24)), code = clip(rint((x - o) / s), 0, 15),
+// two codes per byte, low nibble = even channel), and V as fp16 into the tail
+// at the same row. One workgroup per (kv head, sequence), one lane per
+// channel (a group of 32 channels is half a wave). A sequence whose slot has
+// no valid page is left unchanged.
+template <int D, bool KU4>
+__global__ __launch_bounds__(128) void paged_append_kernel(AkvPagedParams p, const float* __restrict__ knew,
+                                                           const float* __restrict__ vnew, void* __restrict__ kpool,
+                                                           uint16_t* __restrict__ kmeta,
+                                                           const int32_t* __restrict__ table,
+                                                           const int32_t* __restrict__ lens,
+                                                           uint16_t* __restrict__ vtail) {
+    const int c = int(threadIdx.x), kh = int(blockIdx.x), b = int(blockIdx.y);
+    const int Hkv = int(p.kv_heads), P = int(p.page_tokens);
+    const int n = lens[b];
+    if (n < 0 || n / P >= int(p.max_pages)) return;   // uniform over the workgroup
+    const int pid = table[size_t(b) * p.max_pages + n / P];
+    if (pid < 0 || pid >= int(p.num_pages)) return;
+    const int pos = n % P;
+    const size_t src = (size_t(b) * Hkv + kh) * D + c;
+    const size_t row = (size_t(pid) * Hkv + kh) * P + pos;
+    const float x = knew[src];
+    if constexpr (!KU4) {
+        static_cast<uint16_t*>(kpool)[row * D + c] = __builtin_bit_cast(uint16_t, _Float16(x));
+    } else {
+        float mn = x, mx = x;
+#pragma unroll
+        for (int o = 16; o >= 1; o >>= 1) {
+            mn = fminf(mn, __shfl_xor(mn, o, 32));
+            mx = fmaxf(mx, __shfl_xor(mx, o, 32));
+        }
+        const uint16_t ob = fp16_floor_bits(mn);
+        const float o32 = fp16_value(ob);
+        const uint16_t sb = fp16_ceil_bits(fmaxf((mx - o32) / 15.0f, 0x1p-24f));
+        const float s32 = fp16_value(sb);
+        const int code = int(fminf(fmaxf(rintf((x - o32) / s32), 0.0f), 15.0f));
+        const int odd = __shfl_xor(code, 1, 32);
+        if ((c & 1) == 0) static_cast<uint8_t*>(kpool)[row * (D / 2) + c / 2] = uint8_t(code | (odd << 4));
+        if ((c & 31) == 0) {
+            kmeta[(row * (D / 32) + c / 32) * 2] = ob;
+            kmeta[(row * (D / 32) + c / 32) * 2 + 1] = sb;
+        }
+    }
+    vtail[((size_t(b) * Hkv + kh) * P + pos) * D + c] = __builtin_bit_cast(uint16_t, _Float16(vnew[src]));
+}
+
+// Encoded V pages into their pool slots: staging page i (blocks
+// [n][kv_heads][P/block_y][atlas_cols], scale and offset fp16 [n][kv_heads][P])
+// -> pool page ids[i], as 16-byte words. Out-of-range ids are skipped.
+__global__ __launch_bounds__(kThreads) void paged_commit_kernel(const int32_t* __restrict__ ids, uint32_t num_pages,
+                                                                const uint4* __restrict__ blocks,
+                                                                const uint4* __restrict__ scale,
+                                                                const uint4* __restrict__ offset, uint32_t block_words,
+                                                                uint32_t meta_words, uint4* __restrict__ vblocks,
+                                                                uint4* __restrict__ vscale,
+                                                                uint4* __restrict__ voffset) {
+    const uint32_t i = blockIdx.y;
+    const int pid = ids[i];
+    if (pid < 0 || uint32_t(pid) >= num_pages) return;
+    const uint32_t total = block_words + 2 * meta_words;
+    for (uint32_t w = blockIdx.x * kThreads + threadIdx.x; w < total; w += gridDim.x * kThreads) {
+        if (w < block_words) {
+            vblocks[size_t(pid) * block_words + w] = blocks[size_t(i) * block_words + w];
+        } else if (w < block_words + meta_words) {
+            const uint32_t m = w - block_words;
+            vscale[size_t(pid) * meta_words + m] = scale[size_t(i) * meta_words + m];
+        } else {
+            const uint32_t m = w - block_words - meta_words;
+            voffset[size_t(pid) * meta_words + m] = offset[size_t(i) * meta_words + m];
+        }
+    }
+}
+
 // --- host ---------------------------------------------------------------------
 
-int check_paged(const AkvPagedParams* p, uint32_t* G) {
+// The pools' geometry (what the append and commit entry points need too).
+int check_pool(const AkvPagedParams* p) {
     if (!p) return AKV_HIP_ERR_NULL;
-    if (p->batch == 0 || p->max_tokens == 0 || p->kv_heads == 0 || p->query_heads % p->kv_heads)
-        return AKV_HIP_ERR_SHAPE;
-    if (p->dim != 64 && p->dim != 128) return AKV_HIP_ERR_SHAPE;
-    const uint32_t g = p->query_heads / p->kv_heads;
-    if (g != 1 && g != 2 && g != 3 && g != 4 && g != 8) return AKV_HIP_ERR_SHAPE;
-    if (p->batch > 65535 || p->kv_heads > 65535 || p->num_pages == 0) return AKV_HIP_ERR_SHAPE;
+    if (p->batch == 0 || p->kv_heads == 0 || (p->dim != 64 && p->dim != 128)) return AKV_HIP_ERR_SHAPE;
+    if (p->batch > 65535 || p->kv_heads > 65535 || p->num_pages == 0 || p->max_pages == 0) return AKV_HIP_ERR_SHAPE;
     if (p->k_format != AKV_K_FP16 && p->k_format != AKV_K_U4G32) return AKV_HIP_ERR_SHAPE;
     if (p->layout != AKV_LAYOUT_SCALAR && p->layout != AKV_LAYOUT_RGBA) return AKV_HIP_ERR_SHAPE;
     const uint32_t bx = p->block_x, by = p->block_y;
@@ -296,6 +393,15 @@ int check_paged(const AkvPagedParams* p, uint32_t* G) {
     if (p->atlas_cols != (texcols + bx - 1) / bx) return AKV_HIP_ERR_SHAPE;
     const uint32_t P = p->page_tokens;
     if (P == 0 || P % 16 || P % by || P > 4096) return AKV_HIP_ERR_SHAPE;
+    return 0;
+}
+
+int check_paged(const AkvPagedParams* p, uint32_t* G) {
+    if (int rc = check_pool(p)) return rc;
+    if (p->max_tokens == 0 || p->query_heads % p->kv_heads) return AKV_HIP_ERR_SHAPE;
+    const uint32_t g = p->query_heads / p->kv_heads;
+    if (g != 1 && g != 2 && g != 3 && g != 4 && g != 8) return AKV_HIP_ERR_SHAPE;
+    const uint32_t by = p->block_y, P = p->page_tokens;
     if (uint64_t(p->max_pages) * P < p->max_tokens) return AKV_HIP_ERR_SHAPE;
     const uint32_t T = p->tile_tokens;
     if (T == 0 || T % 16 || T % by) return AKV_HIP_ERR_TILE;
@@ -414,6 +520,48 @@ int akv_hip_paged_decode_attention(const AkvPagedParams* p, const float* q, cons
                       seq_lens, v_tail, tab, partial, reinterpret_cast<float2*>(stats), out, arrivals};
     hipStream_t st = static_cast<hipStream_t>(stream);
     return as_int(p->k_format == AKV_K_U4G32 ? launch_paged<true>(a, G, x, st) : launch_paged<false>(a, G, x, st));
+}
+
+int akv_hip_paged_append(const AkvPagedParams* p, const float* k_new, const float* v_new, void* k_pages,
+                         uint16_t* k_meta, const int32_t* block_table, const int32_t* seq_lens, uint16_t* v_tail,
+                         void* stream) {
+    if (int rc = check_pool(p)) return rc;
+    const bool u4 = p->k_format == AKV_K_U4G32;
+    if (!k_new || !v_new || !k_pages || !block_table || !seq_lens || !v_tail || (u4 && !k_meta))
+        return AKV_HIP_ERR_NULL;
+    const dim3 grid(p->kv_heads, p->batch), block(p->dim);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    void* kp = k_pages;
+    if (p->dim == 64) {
+        if (u4) paged_append_kernel<64, true><<<grid, block, 0, st>>>(*p, k_new, v_new, kp, k_meta, block_table, seq_lens, v_tail);
+        else paged_append_kernel<64, false><<<grid, block, 0, st>>>(*p, k_new, v_new, kp, k_meta, block_table, seq_lens, v_tail);
+    } else {
+        if (u4) paged_append_kernel<128, true><<<grid, block, 0, st>>>(*p, k_new, v_new, kp, k_meta, block_table, seq_lens, v_tail);
+        else paged_append_kernel<128, false><<<grid, block, 0, st>>>(*p, k_new, v_new, kp, k_meta, block_table, seq_lens, v_tail);
+    }
+    return as_int(hipGetLastError());
+}
+
+int akv_hip_paged_commit_pages(const AkvPagedParams* p, uint32_t n, const int32_t* page_ids, const void* blocks,
+                               const uint16_t* scale, const uint16_t* offset, void* v_blocks, uint16_t* v_scale,
+                               uint16_t* v_offset, void* stream) {
+    if (int rc = check_pool(p)) return rc;
+    if (n == 0) return 0;
+    if (n > 65535) return AKV_HIP_ERR_SHAPE;
+    if (!page_ids || !blocks || !scale || !offset || !v_blocks || !v_scale || !v_offset) return AKV_HIP_ERR_NULL;
+    if (!aligned16(blocks) || !aligned16(scale) || !aligned16(offset) || !aligned16(v_blocks) ||
+        !aligned16(v_scale) || !aligned16(v_offset))
+        return AKV_HIP_ERR_ALIGN;
+    const uint64_t bw = uint64_t(p->kv_heads) * (p->page_tokens / p->block_y) * p->atlas_cols;
+    const uint64_t mw = uint64_t(p->kv_heads) * p->page_tokens / 8;   // fp16 x P, P a multiple of 16
+    if (bw + 2 * mw > 0xFFFFFFFFull) return AKV_HIP_ERR_SHAPE;
+    const uint32_t total = uint32_t(bw + 2 * mw);
+    const dim3 grid(std::min<uint32_t>((total + kThreads - 1) / kThreads, 64u), n);
+    paged_commit_kernel<<<grid, kThreads, 0, static_cast<hipStream_t>(stream)>>>(
+        page_ids, p->num_pages, static_cast<const uint4*>(blocks), reinterpret_cast<const uint4*>(scale),
+        reinterpret_cast<const uint4*>(offset), uint32_t(bw), uint32_t(mw), static_cast<uint4*>(v_blocks),
+        reinterpret_cast<uint4*>(v_scale), reinterpret_cast<uint4*>(v_offset));
+    return as_int(hipGetLastError());
 }
 
 int akv_hip_paged_task_tokens(const AkvPagedParams* p) {

@@ -181,6 +181,37 @@ int akv_hip_paged_decode_attention(const AkvPagedParams* p, const float* q, cons
                                    const uint16_t* v_tail, float* partial, float* stats, float* out,
                                    uint32_t* arrivals, void* stream);
 
+/* Appending to the paged cache (the active path the reference plans: an FP16
+   fresh tail read by the same split-K, and on page completion a GPU upload of
+   the encoded blocks with no re-encode, docs/representation_v0.1.md:84-95).
+
+   akv_hip_paged_append writes one new token per sequence: k_new, v_new f32
+   [batch][kv_heads][dim] go to row seq_lens[b] % page_tokens of page
+   block_table[b][seq_lens[b] / page_tokens]: K as fp16 (AKV_K_FP16, round to
+   nearest even) or as 4-bit codes plus k_meta computed on the GPU exactly as
+   affine_quantize(axis="token", group=32) in fp32 (AKV_K_U4G32), V as fp16
+   into v_tail (required). seq_lens holds the lengths before the append and is
+   not modified (the caller advances it). A sequence whose slot has no valid
+   page (seq_lens[b] / page_tokens >= max_pages, or an id outside
+   [0, num_pages)) is left unchanged. Uses the pool fields of p (batch,
+   kv_heads, dim, page_tokens, max_pages, num_pages, layout, block_x, block_y,
+   atlas_cols, k_format); inputs finite.
+
+   akv_hip_paged_commit_pages copies n pages the host has encoded (blocks
+   [n][kv_heads][page_tokens/block_y][atlas_cols] 16-byte ASTC blocks, scale
+   and offset fp16 [n][kv_heads][page_tokens], device memory) into the V pool
+   pages page_ids[0..n) (device int32; ids outside [0, num_pages) are
+   skipped), in one launch. A sequence whose length reaches a multiple of
+   page_tokens needs its completed page committed before the next decode step
+   reads it, and before the next append overwrites its tail. */
+int akv_hip_paged_append(const AkvPagedParams* p, const float* k_new, const float* v_new, void* k_pages,
+                         uint16_t* k_meta, const int32_t* block_table, const int32_t* seq_lens, uint16_t* v_tail,
+                         void* stream);
+
+int akv_hip_paged_commit_pages(const AkvPagedParams* p, uint32_t n, const int32_t* page_ids, const void* blocks,
+                               const uint16_t* scale, const uint16_t* offset, void* v_blocks, uint16_t* v_scale,
+                               uint16_t* v_offset, void* stream);
+
 /* Host-side planning query for the paged kernel (no GPU work): tokens per
    chunk, or a negative AKV_HIP_* code. */
 int akv_hip_paged_task_tokens(const AkvPagedParams* p);

@@ -104,6 +104,37 @@ def test_misaligned_pointers_rejected_before_any_launch(hip, bad):
     assert b"16-byte" in hip.akv_hip_error_string(-5)
 
 
+class PagedParams(ct.Structure):
+    _fields_ = [(name, ct.c_uint32) for name in (
+        "batch", "max_tokens", "query_heads", "kv_heads", "dim", "page_tokens", "max_pages", "num_pages",
+        "tile_tokens", "splits", "layout", "block_x", "block_y", "atlas_cols", "k_format")]
+
+
+def test_append_and_commit_validation(hip):
+    # Host-side checks only (no launch): fake device addresses.
+    ap, cm = hip.akv_hip_paged_append, hip.akv_hip_paged_commit_pages
+    ap.argtypes = [ct.POINTER(PagedParams)] + [ct.c_void_p] * 8
+    cm.argtypes = [ct.POINTER(PagedParams), ct.c_uint32] + [ct.c_void_p] * 8
+    ap.restype = cm.restype = ct.c_int
+    p = PagedParams(batch=4, max_tokens=1000, query_heads=32, kv_heads=8, dim=128, page_tokens=96, max_pages=12,
+                    num_pages=48, tile_tokens=0, splits=0, layout=0, block_x=6, block_y=6, atlas_cols=22,
+                    k_format=1)
+    a = [0x10000 * (i + 1) for i in range(8)]
+    assert ap(None, *a) == -1
+    # arguments: k_new, v_new, k_pages, k_meta, block_table, seq_lens, v_tail, stream
+    assert ap(ct.byref(p), *(a[:6] + [None] + a[7:])) == -1         # the FP16 tail is required
+    assert ap(ct.byref(p), *(a[:3] + [None] + a[4:])) == -1         # 4-bit K needs k_meta
+    bad = PagedParams.from_buffer_copy(p)
+    bad.atlas_cols = 21
+    assert ap(ct.byref(bad), *a) == -2
+    bad = PagedParams.from_buffer_copy(p)
+    bad.page_tokens = 90                                            # not a multiple of 16
+    assert cm(ct.byref(bad), 1, *a) == -2
+    assert cm(ct.byref(p), 0, *a) == 0                              # nothing to copy
+    # arguments: page_ids, blocks, scale, offset, v_blocks, v_scale, v_offset, stream
+    assert cm(ct.byref(p), 1, *(a[:2] + [a[2] + 8] + a[3:])) == -5   # staging scale not 16-byte aligned
+
+
 def test_null_params_and_error_strings(hip):
     assert hip.akv_hip_task_tokens(None, 1) == -1
     assert hip.akv_hip_error_string(0) == b"success"

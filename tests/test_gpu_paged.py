@@ -107,3 +107,69 @@ def test_long_splits_many_chunks(gpu):
         ki, vi = host_kv(pk, i)
         ref = R.decode_attention(q[i:i + 1], ki[None], vi[None])[0]
         np.testing.assert_allclose(out[i], ref, rtol=RTOL, atol=ATOL, err_msg=f"sequence {i}")
+
+
+APPEND_CASES = [
+    # layout, block, page, dim, hkv, k_format
+    ("scalar", (6, 6), 96, 128, 2, "u4g32"),
+    ("rgba", (6, 5), 80, 64, 3, "fp16"),
+    ("rgba", (4, 4), 64, 64, 2, "u4g32"),
+]
+
+
+@pytest.mark.parametrize("layout,block,page,d,hkv,kf", APPEND_CASES)
+def test_append_matches_scratch_build(gpu, layout, block, page, d, hkv, kf):
+    """Token-by-token appends (akv_hip_paged_append, with the pages they
+    complete encoded on the host and committed by akv_hip_paged_commit_pages)
+    leave exactly the pools build_paged makes from the whole sequences: K (4-bit
+    codes and fp16 offset/scale computed on the GPU), V blocks, scale/offset and
+    tail, bit for bit, and the same decode output. V is fp16-valued, as the
+    tail keeps it."""
+    from astc_kv.paged import build_paged
+    P = page
+    print(f"append case {layout} {block} P{P} D{d} {kf}", flush=True)
+    rng = np.random.default_rng(P + d)
+    start = [P - 2, 2 * P - 1, 3, P, 1]
+    A = P + 3                              # every sequence completes at least one page
+    full = [t + A for t in start]
+    k = [rng.normal(size=(hkv, t, d)).astype(np.float32) * np.float32(3) for t in full]
+    v = [rng.normal(0, 0.5, size=(hkv, t, d)).astype(np.float16).astype(np.float32) for t in full]
+    spare = 2 * P
+    pk0 = build_paged([x[:, :t] for x, t in zip(k, start)], [x[:, :t] for x, t in zip(v, start)], layout, block, P,
+                      quality=20, k_format=kf, tail=True, seed=7, reserve_tokens=A + spare)
+    ref = build_paged(k, v, layout, block, P, quality=20, k_format=kf, tail=True, seed=7, reserve_tokens=spare)
+    assert np.array_equal(pk0.block_table, ref.block_table)   # the same page assignment
+    cache = gpu.DevicePagedKV.from_host(pk0)
+    completed = 0
+    for j in range(A):
+        kn = torch.from_numpy(np.stack([x[:, t + j] for x, t in zip(k, start)])).cuda()
+        vn = torch.from_numpy(np.stack([x[:, t + j] for x, t in zip(v, start)])).cuda()
+        completed += len(cache.append(kn, vn, quality=20))
+    assert completed == sum((t + A) // P - t // P for t in start)
+    assert cache.lens == full and cache.seq_lens.cpu().tolist() == full
+    assert np.array_equal(cache.k_pages.cpu().numpy(), ref.k_pages)
+    if kf == "u4g32":
+        assert np.array_equal(cache.k_meta.cpu().numpy(), ref.k_meta)
+    assert np.array_equal(cache.v_blocks.cpu().numpy(), ref.v_blocks)
+    assert np.array_equal(cache.v_scale.cpu().numpy(), ref.v_scale)
+    assert np.array_equal(cache.v_offset.cpu().numpy(), ref.v_offset)
+    tail = cache.v_tail.cpu().numpy()
+    for i, t in enumerate(full):
+        assert np.array_equal(tail[i, :, :t % P], ref.v_tail[i, :, :t % P])
+    q = torch.from_numpy(rng.normal(size=(len(full), 4 * hkv, d)).astype(np.float32)).cuda()
+    out_a = gpu.paged_decode_attention(q, cache)
+    out_b = gpu.paged_decode_attention(q, gpu.DevicePagedKV.from_host(ref))
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, out_b)
+
+
+def test_append_needs_a_reserved_page(gpu):
+    from astc_kv.paged import build_paged
+    rng = np.random.default_rng(11)
+    k = [rng.normal(size=(1, 64, 64)).astype(np.float16)]
+    v = [rng.normal(0, 0.5, size=(1, 64, 64)).astype(np.float32)]
+    cache = gpu.DevicePagedKV.from_host(build_paged(k, v, "rgba", (4, 4), 64, quality=10, tail=True))
+    x = torch.zeros((1, 1, 64), dtype=torch.float32, device="cuda")
+    with pytest.raises(ValueError, match="no page"):
+        cache.append(x, x)
+    assert cache.lens == [64]

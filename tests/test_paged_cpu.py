@@ -63,3 +63,37 @@ def test_rejects_bad_pages():
         build_paged(k, v, "rgba", (6, 5), 40)          # not a multiple of 16
     with pytest.raises(ValueError):
         build_paged(k, v, "rgba", (6, 5), 48)          # not a multiple of the block height
+
+
+@pytest.mark.parametrize("layout,block", [("rgba", (6, 5)), ("scalar", (6, 6))])
+def test_pagewise_encoding_equals_whole_sequence(layout, block):
+    # The append path encodes each completed page on its own (from the FP16
+    # tail) and copies the blocks into the pool; that equals encoding the whole
+    # sequence because a page is whole block rows and normalization is per token.
+    rng = np.random.default_rng(5)
+    P = 120 if block == (6, 5) else 96
+    v = rng.normal(0, 0.5, size=(2, 3 * P, 64)).astype(np.float16).astype(np.float32)
+    whole = build_atlas(v[None], layout, block, P, 20)
+    pages = build_atlas(v.reshape(2, 3, P, 64).transpose(1, 0, 2, 3), layout, block, P, 20)
+    rpp = P // block[1]
+    for j in range(3):
+        assert np.array_equal(pages.blocks[j], whole.blocks[0, :, j * rpp:(j + 1) * rpp])
+        assert np.array_equal(pages.scale[j], whole.scale[0, :, j * P:(j + 1) * P])
+        assert np.array_equal(pages.offset[j], whole.offset[0, :, j * P:(j + 1) * P])
+
+
+def test_reserved_pages_for_appends():
+    rng = np.random.default_rng(2)
+    lens = [50, 96, 97]
+    k, v = _seqs(rng, lens)
+    P = 48
+    pk = build_paged(k, v, "rgba", (4, 4), P, quality=10, tail=True, seed=1, reserve_tokens=60)
+    pages = [-(-(t + 60) // P) for t in lens]
+    assert pk.block_table.shape == (3, max(pages)) and pk.k_pages.shape[0] == sum(pages)
+    used = np.concatenate([pk.block_table[i, :n] for i, n in enumerate(pages)])
+    assert sorted(used.tolist()) == list(range(sum(pages)))
+    for i, t in enumerate(lens):                       # reserved pages stay empty
+        empty = pk.block_table[i, -(-t // P):pages[i]]
+        assert not pk.k_pages[empty].any() and not pk.v_blocks[empty].any()
+    with pytest.raises(ValueError):
+        build_paged(k, v, "rgba", (4, 4), P, reserve_tokens=-1)
