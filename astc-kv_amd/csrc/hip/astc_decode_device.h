@@ -254,11 +254,19 @@ __device__ __attribute__((always_inline)) inline void ise_unpack(const uint32_t 
 
 // Colour values of range R (4..20): at most 18, and never more than fit in the
 // 111 bits after the 17-bit header.
+// The values are packed four to a dword (value j in byte j % 4 of dword
+// j / 4) and stored as dwords: ColourScratch.
 template <int R>
 __device__ __attribute__((always_inline)) inline void colour_values(const uint32_t (&s)[4], const LdsTables& L,
-                                                                    uint8_t* cv) {
+                                                                    uint32_t* cv) {
     constexpr int V = ise_max_values(R, 18, 111);
-    ise_unpack<R, V>(s, L, [&](auto ji, uint32_t v) { cv[decltype(ji)::value] = L.color_unq[R][v]; });
+    uint32_t w[(V + 3) / 4] = {};
+    ise_unpack<R, V>(s, L, [&](auto ji, uint32_t v) {
+        constexpr int j = decltype(ji)::value;
+        w[j / 4] |= uint32_t(L.color_unq[R][v]) << (8 * (j % 4));
+    });
+#pragma unroll
+    for (int i = 0; i < (V + 3) / 4; ++i) cv[i] = w[i];
 }
 
 // Weight fields of trit/quint range R as plain nb-bit fields (nb = bits + 2
@@ -281,9 +289,9 @@ __device__ __attribute__((always_inline)) inline void weight_fields(const uint32
 }
 
 // Colour integer sequence of this lane's block: range `crange`, `nv` values
-// from bit `start` of the block `blk` (four words in LDS) -> cv[0..].
+// from bit `start` of the block `blk` (four words in LDS) -> cv (packed bytes).
 __device__ __attribute__((always_inline)) inline void decode_colour_values(const uint32_t* blk, int start, int crange, int nv, const LdsTables& L,
-                                            uint8_t* cv) {
+                                            uint32_t* cv) {
     const uint4 b4 = *reinterpret_cast<const uint4*>(blk);
     while (true) {
         const int r = __builtin_amdgcn_readfirstlane(crange);
@@ -362,12 +370,21 @@ __device__ inline void bit_transfer(int& offset, int& base) {
     if (offset & 0x20) offset -= 0x40;
 }
 
-// Endpoint decode of one partition from its unquantised colour values
-// cv[k..]: 8-bit RGBA pairs. False for HDR modes.
-__device__ inline bool cem_endpoints(int cem, const uint8_t* cv, int k, int* e0, int* e1) {
+// Endpoint decode of one partition from its unquantised colour values, bytes
+// k .. k + 7 of the packed scratch (k even, at most 16: three dword reads and
+// two byte alignments; the dword past a window that starts on a dword
+// boundary is not needed, so the read index is clamped to the scratch).
+// 8-bit RGBA pairs. False for HDR modes.
+constexpr int kColourScratchWords = 6;   // 18 values, and the window's third dword
+__device__ inline bool cem_endpoints(int cem, const uint32_t* cv, int k, int* e0, int* e1) {
+    const int k4 = k >> 2;
+    const uint32_t a = cv[k4], b = cv[k4 + 1], c = cv[min(k4 + 2, kColourScratchWords - 1)];
+    const uint32_t lo = __builtin_amdgcn_alignbyte(b, a, uint32_t(k & 3));
+    const uint32_t hi = __builtin_amdgcn_alignbyte(c, b, uint32_t(k & 3));
     int v[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = (j < 2 * ((cem >> 2) + 1)) ? int(cv[k + j]) : 0;
+    for (int j = 0; j < 8; ++j)
+        v[j] = (j < 2 * ((cem >> 2) + 1)) ? int(((j < 4 ? lo : hi) >> (8 * (j % 4))) & 0xFFu) : 0;
     switch (cem) {
         case 0:
             e0[0] = e0[1] = e0[2] = v[0]; e0[3] = 255;
@@ -471,6 +488,25 @@ __device__ inline void put_entry(uint32_t* tab, int entry, const uint32_t* ep, u
         tab[2 * entry + 1] = pack_fp16_rtz(interp_c(ep[2], wp), interp_c(ep[3], wp));
     } else {
         reinterpret_cast<uint16_t*>(tab)[entry] = uint16_t(pack_fp16_rtz(interp_c(ep[0], wp), 0));
+    }
+}
+
+// Table entry of weight 0 (sh = 0, endpoint e0) or 64 (sh = 16, e1): interp_c
+// of such a weight is the endpoint e itself, except 0xFFFF -> 0x10000 (FP16
+// 1.0).
+template <int NCH>
+__device__ inline void put_end_entry(uint32_t* tab, int entry, const uint32_t* ep, int sh) {
+    uint32_t C[NCH];
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+        const uint32_t e = (ep[ch] >> sh) & 0xFFFFu;
+        C[ch] = e + ((e + 1) >> 16);
+    }
+    if constexpr (NCH == 4) {
+        tab[2 * entry] = pack_fp16_rtz(C[0], C[1]);
+        tab[2 * entry + 1] = pack_fp16_rtz(C[2], C[3]);
+    } else {
+        reinterpret_cast<uint16_t*>(tab)[entry] = uint16_t(pack_fp16_rtz(C[0], 0));
     }
 }
 
@@ -581,11 +617,12 @@ __device__ inline uint4 block_part_words(uint4 raw, uint4 words, int key) {
 }
 
 // Stage 1: one lane decodes the block stashed in `d` (stash_block) into `d`.
-// `cv` is this lane's 20-byte scratch for the unquantised colour values.
+// `cv` is this lane's scratch for the unquantised colour values
+// (kColourScratchWords dwords, four values per dword).
 // Every table read is from LDS.
 template <int NCH>
 __device__ __attribute__((always_inline)) inline void decode_header(const LdsTables& L, BlockDesc<NCH>& d,
-                                                                   uint8_t* cv) {
+                                                                   uint32_t* cv) {
     const uint32_t* blk = d.tab;        // block bits
     const uint32_t* rev = d.tab + 8;    // weight stream
     const uint32_t w0 = blk[0];
@@ -680,8 +717,12 @@ __device__ __attribute__((always_inline)) inline void decode_header(const LdsTab
         k += 2 * ((cem >> 2) + 1);
         if (table) {
             // One row of `levels` entries per partition (parts * levels fits).
+            // Entries are indexed by the raw weight field, whose order is not
+            // the weights' order for trit and quint ranges with extra bits;
+            // field 0 always unquantises to weight 0, i.e. endpoint e0.
+            put_end_entry<NCH>(d.tab, p * levels, ep, 0);
 #pragma unroll
-            for (int q = 0; q < BlockDesc<NCH>::kTabEntries; ++q) {
+            for (int q = 1; q < BlockDesc<NCH>::kTabEntries; ++q) {
                 if (q >= levels) break;
                 put_entry<NCH>(d.tab, p * levels + q, ep, weight_pair(L.weight_unq[wrange][q]));
             }

@@ -535,7 +535,7 @@ struct AstcShared {
     union {
         struct {
             BlockDesc<NCH> desc[C::kMaxBlocks];
-            uint8_t cv[C::kMaxBlocks][20];   // colour values of the header stage, per lane
+            uint32_t cv[C::kMaxBlocks][kColourScratchWords];   // header-stage colour values, per lane
         } h;
         float comb[kWaves * D * kMaxG];      // final per-wave accumulators
     } u;

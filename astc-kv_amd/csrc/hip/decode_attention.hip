@@ -364,7 +364,7 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(uint32_t splits, uint32
 struct BlocksShared {
     LdsTables tabs;
     BlockDesc<4> desc[kThreads];
-    uint8_t cv[kThreads][20];
+    uint32_t cv[kThreads][kColourScratchWords];
 };
 
 // 256 blocks per workgroup -> FP16 RGBA texels [n][by][bx][4].
