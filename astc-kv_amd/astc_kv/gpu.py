@@ -111,7 +111,7 @@ def task_tokens(params: AkvAttnParams, astc: bool = True) -> int:
 
 def default_tile(batch: int, kv_heads: int, tokens: int, chunk: int, block: int = 1, cu_count: int = 256,
                  groups_per_cu: int = 3, overhead_tokens: int = 64) -> int:
-    """Tokens per split (a multiple of `block`, the footprint height).
+    """Tokens per split (a multiple of `block`: 16 for the kernels here).
 
     * Fewer chunks than CUs: splits of about tokens * batch * kv_heads / CUs
       tokens (at least 16) for parallelism.
@@ -143,9 +143,10 @@ def default_tile(batch: int, kv_heads: int, tokens: int, chunk: int, block: int 
 
 
 def tile_for_splits(tokens: int, splits: int, block_y: int, dim: int) -> int:
-    """Tile giving exactly `splits` splits when possible (e.g. T2048 in 8 splits)."""
+    """Tile giving exactly `splits` splits when possible (e.g. T2048 in 8
+    splits); tiles are multiples of 16 tokens (block_y is not a constraint)."""
     tile = -(-tokens // splits)
-    return -(-tile // block_y) * block_y
+    return -(-tile // 16) * 16
 
 
 @dataclass
@@ -196,9 +197,9 @@ def make_params(atlas: DeviceAtlas, query_heads: int, tile: int | None = None) -
                              atlas.blocks.shape[2], cols)
 
     if tile is None:
-        whole = -(-atlas.tokens // atlas.block_y) * atlas.block_y   # one split: the chunk is not clipped
+        whole = -(-atlas.tokens // 16) * 16   # one split: the chunk is not clipped
         # Resident workgroups per CU: three at head dim 64, two at 128 (registers).
-        tile = default_tile(b, h, atlas.tokens, task_tokens(build(whole)), atlas.block_y,
+        tile = default_tile(b, h, atlas.tokens, task_tokens(build(whole)), 16,
                             groups_per_cu=3 if atlas.dim == 64 else 2)
     return build(tile)
 

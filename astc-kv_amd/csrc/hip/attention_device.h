@@ -585,11 +585,13 @@ __device__ __attribute__((always_inline)) inline void column_texels(const BlockD
 }
 
 // Row table of a chunk: token t -> (first block of its block row) << 16 |
-// (y * bx) << 8 | y, y = t % by. Tokens at or past ntok take the entry of the
-// chunk's last token, so that tile padding decodes real (finite) texels; their
-// probabilities are zero.
-__device__ inline uint32_t token_row_entry(int t, int ntok, uint32_t mag_by, Footprint f, uint32_t cols) {
-    const int tl = min(t, ntok - 1);
+// (y * bx) << 8 | y, for a chunk whose first token sits at row offset yoff
+// of its first block row (y = (t + yoff) % by). Tokens at or past ntok take
+// the entry of the chunk's last token, so that tile padding decodes real
+// (finite) texels; their probabilities are zero.
+__device__ inline uint32_t token_row_entry(int t, int ntok, uint32_t mag_by, Footprint f, uint32_t cols,
+                                           int yoff = 0) {
+    const int tl = min(t, ntok - 1) + yoff;
     const int r = int(fdiv(uint32_t(tl), mag_by)), y = tl - r * f.by;
     return (__umul24(uint32_t(r), cols) << 16) | (uint32_t(y * f.bx) << 8) | uint32_t(y);
 }

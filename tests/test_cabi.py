@@ -53,16 +53,19 @@ def c3(**kw):
 
 
 def test_chunk_tokens_follow_the_footprint(hip):
-    # 6x5 RGBA D64: 3 block columns, at most 160 blocks -> 53 block rows = 265 tokens.
-    assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=8190, splits=2)), 1) == 265
+    # 6x5 RGBA D64: 3 block columns, at most 160 blocks -> 53 block rows; a
+    # chunk starts on a 16-token boundary, at most 4 tokens into its first
+    # row, so 261 tokens fit; 256 = 16 tiles, the same number for every wave.
+    assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=8192, splits=1)), 1) == 256
     # A split shorter than a chunk is one chunk.
-    assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=35, splits=235)), 1) == 35
+    assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=48, splits=171)), 1) == 48
     # 4x4 RGBA D64: 4 block columns -> 40 block rows = 160 tokens.
     p = c3(block_x=4, block_y=4, atlas_cols=4, atlas_rows=2048, tile_tokens=8192, splits=1)
     assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 160
-    # Scalar 6x6 D64: 11 block columns -> 14 rows = 84 tokens.
-    p = c3(layout=0, block_x=6, block_y=6, atlas_cols=11, atlas_rows=1366, tile_tokens=8196, splits=1)
-    assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 84
+    # Scalar 6x6 D64: 11 block columns -> 14 rows = 84 tokens, at most 4 in
+    # at the start -> 80.
+    p = c3(layout=0, block_x=6, block_y=6, atlas_cols=11, atlas_rows=1366, tile_tokens=8192, splits=1)
+    assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 80
     # D128 RGBA 4x4: 8 block columns, at most 256 blocks -> 32 rows = 128 tokens.
     p = c3(dim=128, block_x=4, block_y=4, atlas_cols=8, atlas_rows=2048, tile_tokens=8192, splits=1)
     assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 128
@@ -81,7 +84,7 @@ def test_chunk_tokens_follow_the_footprint(hip):
     (dict(layout=7), -2),
     (dict(block_x=3), -3),                            # footprint below 4
     (dict(block_x=10, block_y=8, atlas_cols=2), -3),  # more than 64 texels
-    (dict(tile_tokens=238, splits=35), -4),           # tile not a multiple of block_y
+    (dict(tile_tokens=238, splits=35), -4),           # tile not a multiple of 16
     (dict(splits=34), -4),                            # splits != ceil(T / tile)
     (dict(tile_tokens=0), -4),
 ])
@@ -100,7 +103,7 @@ def test_misaligned_pointers_rejected_before_any_launch(hip, bad):
     ptr = {"q": 0x10000, "k": 0x20000, "v": 0x30000}
     ptr[bad] += 4
     args = [ptr["q"], ptr["k"], ptr["v"], 0x40000, 0x50000, 0x60000, 0x70000, 0x80000, None]
-    assert fn(ct.byref(c3(tile_tokens=515, splits=16)), *args) == -5
+    assert fn(ct.byref(c3(tile_tokens=512, splits=16)), *args) == -5
     assert b"16-byte" in hip.akv_hip_error_string(-5)
 
 

@@ -220,21 +220,20 @@ def test_atlas_layout_and_restore(layout, block, d):
 
 def test_default_tiles():
     from astc_kv.gpu import default_tile, fp16_params, tile_for_splits
-    # c3 (48 sequence x kv-head pairs, 265-token chunks): 16 splits = 768
+    # c3 (48 sequence x kv-head pairs, 256-token chunks): 16 splits = 768
     # workgroups, one round of 3 per CU on 256 CUs (two rounds of one-chunk
-    # splits cost 2 x (265 + 64) > 515 + 64); the shortest such tile in whole
-    # 5-token block rows.
-    t = default_tile(16, 3, 8192, 265, 5)
-    assert t == 515 and 48 * -(-8192 // t) == 768
+    # splits cost 2 x (256 + 64) > 512 + 64): two whole chunks per split.
+    t = default_tile(16, 3, 8192, 256, 16)
+    assert t == 512 and 48 * -(-8192 // t) == 768
     # 4x4 (160-token chunks): one full round of 16 splits.
-    t = default_tile(16, 3, 8192, 160, 4)
-    assert t % 4 == 0 and 512 <= t <= 528 and 48 * -(-8192 // t) == 768
+    t = default_tile(16, 3, 8192, 160, 16)
+    assert t % 16 == 0 and t == 512 and 48 * -(-8192 // t) == 768
     # c4 (64 pairs, 80-token chunks, > 8 rounds): several chunks per split.
     t = default_tile(8, 8, 32768, 80, 4)
     assert t % 80 == 0 and 80 < t <= 8 * 80
-    # Tiny workloads: split for parallelism, in whole block rows, never above a chunk.
-    t = default_tile(1, 3, 384, 265, 5)
-    assert t % 5 == 0 and 16 <= t <= 265
-    assert tile_for_splits(2048, 8, 6, 64) == 258 and -(-2048 // 258) == 8
+    # Tiny workloads: split for parallelism, in whole tiles, never above a chunk.
+    t = default_tile(1, 3, 384, 256, 16)
+    assert t % 16 == 0 and 16 <= t <= 256
+    assert tile_for_splits(2048, 8, 6, 64) == 256 and -(-2048 // 256) == 8
     p = fp16_params(16, 3, 9, 8192, 64)
     assert p.tile_tokens == 512 and p.splits == 16

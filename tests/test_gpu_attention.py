@@ -62,7 +62,7 @@ def test_fixture_attention(gpu, golden, name, T):
     k = np.fromfile(golden / name / "k.f16", "<f2").reshape(1, 3, T, 64)
     v_ref = np.fromfile(golden / name / "v_decoded.f32", "<f4").reshape(1, 3, T, 64)
     assert np.array_equal(oracle_v(atlas).view(np.uint32), v_ref.view(np.uint32))
-    for tile in (6, 30, 36, 96, 252):
+    for tile in (16, 32, 48, 96, 256):
         check(run(gpu, q, k, atlas, tile), q, k, v_ref)
 
 
@@ -107,7 +107,7 @@ def test_synthetic_attention(gpu, layout, block, b, hq, hkv, t, d, heavy):
     q, k, v = synthetic(rng, b, hq, hkv, t, d, heavy=heavy)
     atlas = build_atlas(v, layout, block, page_tokens=120, quality=40)
     vr = oracle_v(atlas)
-    for tile in (None, block[1] * 4):
+    for tile in (None, 64):
         check(run(gpu, q, k, atlas, tile), q, k, vr)
 
 
@@ -118,7 +118,7 @@ def test_split_states_match_oracle(gpu, golden):
     atlas, _ = atlas_from_manifest(golden / "t391")
     q = np.fromfile(golden / "t391" / "q.f32", "<f4").reshape(1, 9, 64)
     k = np.fromfile(golden / "t391" / "k.f16", "<f2").reshape(1, 3, 391, 64)
-    tile = 36
+    tile = 48
     out, partial, stats = gpu.decode_attention(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(),
                                                DeviceAtlas.from_host(atlas), tile, return_states=True)
     partial, stats = partial.cpu().numpy()[0], stats.cpu().numpy()[0]
@@ -182,7 +182,7 @@ def test_fused_merge_matches_two_launches(gpu):
     q, k, v = synthetic(rng, 3, 9, 3, 1200, 64)
     dev = DeviceAtlas.from_host(build_atlas(v, "rgba", (6, 5), page_tokens=120, quality=30))
     qt, kt = torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda()
-    for tile in (None, 60, 265):
+    for tile in (None, 64, 272):
         two = gpu.decode_attention(qt, kt, dev, tile, fused=False).cpu().numpy()
         outs = [gpu.decode_attention(qt, kt, dev, tile).cpu().numpy() for _ in range(3)]
         for o in outs:

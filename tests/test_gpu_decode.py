@@ -90,7 +90,7 @@ def _oracle_normalized(atlas):
 def test_decode_values_fixture(gpu, golden, name):
     from astc_kv.atlas import atlas_from_manifest
     atlas, _ = atlas_from_manifest(golden / name)
-    for tile in (6, 36, 96, 252):
+    for tile in (16, 48, 96, 256):
         _atlas_check(gpu, atlas, tile)
 
 
@@ -103,4 +103,4 @@ def test_decode_values_synthetic(gpu, layout, block, dim):
     v = rng.normal(0, 0.5, size=(2, 2, t, dim)).astype(np.float32)
     atlas = build_atlas(v, layout, block, page_tokens=120 if block[1] != 8 else 120, quality=60)
     _atlas_check(gpu, atlas)
-    _atlas_check(gpu, atlas, tile=block[1] * 3)
+    _atlas_check(gpu, atlas, tile=48)
