@@ -46,8 +46,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
     float* partial, float2* stats, uint16_t* __restrict__ dump, float* __restrict__ out, uint32_t* arrivals) {
     using C = Cfg<D, NCH>;
     constexpr int TPG = Grp<G, D>::TPG;
-    // K tiles of a wave's first group requested before the header stage (their
-    // registers are live through it); the rest right after it.
+    // K tiles of a wave's first group: the first kKEarly requested with the
+    // chunk's other loads, the rest just before the header stage (all arrive
+    // during it; issued together they stall the chunk's first phase).
     constexpr int kKEarly = TPG < 2 ? TPG : 2;
     __shared__ AstcShared<D, NCH> sh;
     const AkvAttnParams& p = a.p;
@@ -151,6 +152,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
         place_by_class(sh.key_count, sh.order, key, rank, tid < nblk, tid);
         __syncthreads();   // sorted order complete (and every count read)
         if (wave == 0) sh.key_count[lane] = 0;   // for the next chunk (two barriers away)
+        if constexpr (!DUMP) {
+#pragma unroll
+            for (int t = kKEarly; t < TPG; ++t)
+                load_k_tile<D>(kreg + t * C::kRowLoads, krs, 16 * (TPG * wave + t), lane);
+        }
         if (tid < nblk) decode_header<NCH>(sh.tabs, sh.u.h.desc[sh.order[tid]], sh.u.h.cv[tid]);
         // What the texel stage needs besides the headers: each lane's own
         // block's partition words, and the per-token scale | offset << 16
@@ -195,9 +201,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
                 }
             }
         } else {
-#pragma unroll
-            for (int t = kKEarly; t < TPG; ++t)
-                load_k_tile<D>(kreg + t * C::kRowLoads, krs, 16 * (TPG * wave + t), lane);
 #pragma unroll 1
             for (int tb0 = 16 * TPG * wave; tb0 < ntok; tb0 += 16 * TPG * kWaves) {
                 const int ng = min(TPG, (ntok - tb0 + 15) >> 4);
