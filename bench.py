@@ -73,6 +73,8 @@ def parse_args(argv=None):
     ap.add_argument("--copy-calibration-mb", type=float, default=0.0,
                     help="also run a plain copy kernel over this many MB (for rocprofv3 counter scaling)")
     ap.add_argument("--traffic", default=str(TRAFFIC_FILE), help="profile summary holding the measured traffic")
+    ap.add_argument("--counters", nargs="+", metavar="PMC_DIR",
+                    help="print a table of the PMC counters in these rocprofv3 --pmc output directories")
     ap.add_argument("--summarize", nargs=3, metavar=("KT", "FETCH", "WRITE"),
                     help="print a markdown summary of rocprofv3 CSV output directories and exit")
     ap.add_argument("--out", default="", help="also write the JSON line to this file")
@@ -218,6 +220,29 @@ def _counter_means(directory: str, counter: str):
     return {k: sums[k] / counts[k] for k in sums}
 
 
+def summarize_counters(dirs, kernels=("astc_attn_kernel", "fp16_attn_kernel")) -> str:
+    """Markdown table of every PMC counter found under `dirs` (rocprofv3
+    --pmc output), mean per dispatch, for the kernels whose names start with
+    one of `kernels`."""
+    sums, counts = {}, {}
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                k = _short(r["Kernel_Name"])
+                if not k.startswith(kernels):
+                    continue
+                key = (k, r["Counter_Name"])
+                sums[key] = sums.get(key, 0.0) + float(r["Counter_Value"])
+                counts[key] = counts.get(key, 0) + 1
+    names = sorted({k for k, _ in sums})
+    ctrs = sorted({c for _, c in sums})
+    out = ["| counter | " + " | ".join(f"`{n}`" for n in names) + " |", "|---|" + "---|" * len(names)]
+    for c in ctrs:
+        vals = [f"{sums[(n, c)] / counts[(n, c)]:.4g}" if (n, c) in sums else "" for n in names]
+        out.append(f"| {c} | " + " | ".join(vals) + " |")
+    return "\n".join(out) + "\n"
+
+
 def summarize(kt_dir: str, fetch_dir: str, write_dir: str, calib_mb: float, workload: str) -> str:
     rows = []
     for f in glob.glob(os.path.join(kt_dir, "**", "*kernel_stats.csv"), recursive=True):
@@ -359,6 +384,9 @@ def main(argv=None):
     a = parse_args(argv)
     if a.summarize:
         print(summarize(*a.summarize, a.copy_calibration_mb, workload_name(a)))
+        return 0
+    if a.counters:
+        print(summarize_counters(a.counters))
         return 0
     if a.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported (run with --gpus 1)",
