@@ -1,7 +1,7 @@
 /*
  * ORACLE — test infrastructure only. Nothing in the product links, loads or
  * calls this file; only tests/, __graft_entry__.smoke() and bench.py's CPU
- * baseline leg use it, and only as the checker.
+ * baseline leg use it, and only to check results or as the timed CPU baseline.
  *
  * CPU restatement of ASTC LDR block decoding as performed by Arm astcenc 5.7.0
  * (ARM-software/astc-encoder, tag 5.7.0, Apache-2.0), the codec the reference
