@@ -517,7 +517,10 @@ __device__ inline void set_constant(BlockDesc<NCH>& d, uint32_t r, uint32_t g, u
     uint32_t ep[NCH];
 #pragma unroll
     for (int ch = 0; ch < NCH; ++ch) ep[ch] = c[ch] | (c[ch] << 16);
-    put_entry<NCH>(d.tab, 0, ep, weight_pair(0));
+    // Entries 0..3 all hold the colour: a texel reads entry p (one level,
+    // weight field 0), whatever partition index p the block's bits select.
+#pragma unroll
+    for (int e = 0; e < 4; ++e) put_entry<NCH>(d.tab, e, ep, weight_pair(0));
 #pragma unroll
     for (int i = 0; i < 5; ++i) d.qw[i] = 0;
     d.info = kInfoTable | kInfoIdentity | (1u << kInfoLevelsShift);
@@ -558,60 +561,37 @@ __device__ inline void stash_block(BlockDesc<NCH>& d, uint4 raw) {
     d.tab[12] = 0;
 }
 
-// Decode-path class of a block, 0..kPathKeys-1: blocks of one class take the
-// same branches through decode_header (weight range, partition count and
-// colour range, up to collisions of the fold), so sorting a chunk's blocks by
-// class before the header stage keeps the lanes of a wave on one path. Constant blocks (void
-// extent, reserved or invalid modes, too few colour bits: the blocks
-// decode_header makes constant, by the same tests) are class kPathKeys - 1,
-// and only they are; block_part_words relies on that.
+// Decode-path class of a block, 0..kPathKeys-1, only a sort key: a hash of
+// the bits that fix the block's path through decode_header (block mode,
+// partition count, colour endpoint mode or selector; blocks that agree on
+// them share weight grid and range, colour range and branches), so sorting a
+// chunk's blocks by class keeps the lanes of a wave on one path. Void-extent
+// blocks are class kPathKeys - 1. No table lookups.
 constexpr int kPathKeys = 64;
 
-__device__ inline int block_path_key(uint4 raw, const LdsTables& L) {
+__device__ inline int block_path_key(uint4 raw) {
     const uint32_t mode = raw.x & 0x7FF;
-    const uint32_t md = L.block_mode[mode];
-    const int parts = int((raw.x >> 11) & 3) + 1;
-    if ((mode & 0x1FF) == 0x1FC || !md || (akv::mode_dual(md) && parts == 4)) return kPathKeys - 1;
-    // Colour range as decode_header derives it.
-    int below = 128 - int(akv::mode_wbits(md)) - (akv::mode_dual(md) ? 2 : 0);
-    uint32_t cems;
-    if (parts == 1) {
-        cems = (raw.x >> 13) & 15;
-    } else {
-        const uint32_t sel = (raw.x >> 23) & 0x3F;
-        if ((sel & 3) == 0) {
-            cems = (sel >> 2) * 0x1111u;
-        } else {
-            below -= 3 * parts - 4;
-            // Only the classes matter for the value count: class + "up" bit.
-            const int base_class = int(sel & 3) - 1;
-            cems = 0;
-            for (int p = 0; p < parts; ++p) cems |= uint32_t((base_class + ((sel >> (2 + p)) & 1)) << 2) << (4 * p);
-        }
-    }
-    int pairs = 0;
-    for (int p = 0; p < parts; ++p) pairs += int((cems >> (4 * p)) & 15) / 4 + 1;
-    const int avail = below - (parts == 1 ? 17 : 29);
-    const int crange = (pairs <= 9 && avail > 0) ? int(L.color_range[pairs][min(avail, 127)]) : -1;
-    if (crange < akv::kRange6) return kPathKeys - 1;
-    // (weight range, partition count, colour range) folded onto 63 classes.
-    return ((int(akv::mode_range(md)) * 4 + parts - 1) * 17 + crange - akv::kRange6) % (kPathKeys - 1);
+    if ((mode & 0x1FF) == 0x1FC) return kPathKeys - 1;
+    const uint32_t parts = (raw.x >> 11) & 3;   // partitions - 1
+    const uint32_t sel = parts == 0 ? (raw.x >> 13) & 15 : (raw.x >> 23) & 0x3F;
+    const uint32_t h = (mode | (parts << 11) | (sel << 13)) * 0x9E3779B1u;
+    return int(__umulhi(h, uint32_t(kPathKeys - 1)));   // 0 .. kPathKeys - 2
 }
 
 // The partition-pattern table entry a block's bits select (any 128-bit value
-// selects an in-range entry; which blocks use it, block_part_words decides).
+// selects an in-range entry; block_part_words zeroes it for one partition).
 // A plain load, so that callers can issue it early and use it late.
 __device__ inline uint4 partition_words(uint4 raw, const AkvTables* __restrict__ tab) {
     const int parts = int((raw.x >> 11) & 3) + 1;
     return *reinterpret_cast<const uint4*>(tab->partition[max(parts - 2, 0)][(raw.x >> 13) & 0x3FF]);
 }
 
-// BlockDesc::part of a block: its pattern words, or zero for one partition and
-// for the blocks decode_header turns into a constant colour (void extent,
-// reserved modes, too few colour bits: exactly block_path_key ==
-// kPathKeys - 1), whose one table entry is entry 0.
-__device__ inline uint4 block_part_words(uint4 raw, uint4 words, int key) {
-    const bool zero = ((raw.x >> 11) & 3) == 0 || key == kPathKeys - 1;
+// BlockDesc::part of a block: its pattern words, or zero for one partition.
+// (Blocks that decode_header turns into a constant colour may keep any
+// pattern: their table repeats the colour in every entry a partition index
+// can select.)
+__device__ inline uint4 block_part_words(uint4 raw, uint4 words) {
+    const bool zero = ((raw.x >> 11) & 3) == 0;
     const uint32_t m = zero ? 0u : ~0u;
     return uint4{words.x & m, words.y & m, words.z & m, words.w & m};
 }

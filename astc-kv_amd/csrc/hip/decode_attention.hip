@@ -139,7 +139,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
         // reads them from there and overwrites that slot.
         int key = 0, rank = 0;
         if (tid < nblk) {
-            key = block_path_key(raw_now, sh.tabs);
+            key = block_path_key(raw_now);
             stash_block(sh.u.h.desc[tid], raw_now);
             rank = int(atomicAdd(&sh.key_count[key], 1u));
         }
@@ -162,7 +162,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
         // block's partition words, and the per-token scale | offset << 16
         // (zero past the chunk, up to the tile edge).
         if (tid < nblk) {
-            const uint4 w = block_part_words(raw_now, pat, key);
+            const uint4 w = block_part_words(raw_now, pat);
             uint32_t* part = sh.u.h.desc[tid].part;   // 4-byte aligned
             part[0] = w.x;
             part[1] = w.y;
@@ -389,7 +389,7 @@ __global__ __launch_bounds__(kThreads) void decode_blocks_kernel(const uint4* __
     if (tid < nblk) {
         stash_block(sh.desc[tid], raw);
         decode_header<4>(sh.tabs, sh.desc[tid], sh.cv[tid]);
-        const uint4 w = block_part_words(raw, pw, block_path_key(raw, sh.tabs));
+        const uint4 w = block_part_words(raw, pw);
         uint32_t* part = sh.desc[tid].part;
         part[0] = w.x;
         part[1] = w.y;

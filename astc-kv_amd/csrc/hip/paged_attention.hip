@@ -201,7 +201,7 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
         // decode-path class.
         int key = 0, rank = 0;
         if (tid < nblk) {
-            key = block_path_key(raw_now, sh.tabs);
+            key = block_path_key(raw_now);
             stash_block(sh.u.h.desc[tid], raw_now);
             rank = int(atomicAdd(&sh.key_count[key], 1u));
         }
@@ -220,7 +220,7 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
         // offset << 16 (tail tokens: fp16 1.0 and 0; zero past the chunk, up
         // to the tile edge).
         if (tid < nblk) {
-            const uint4 w = block_part_words(raw_now, pat, key);
+            const uint4 w = block_part_words(raw_now, pat);
             uint32_t* part = sh.u.h.desc[tid].part;   // 4-byte aligned
             part[0] = w.x;
             part[1] = w.y;
