@@ -385,11 +385,27 @@ __device__ inline bool cem_endpoints(int cem, const uint32_t* cv, int k, int* e0
 #pragma unroll
     for (int j = 0; j < 8; ++j)
         v[j] = (j < 2 * ((cem >> 2) + 1)) ? int(((j < 4 ? lo : hi) >> (8 * (j % 4))) & 0xFFu) : 0;
+    // The common modes first (RGB(A) direct, luminance direct): in a wave
+    // whose lanes all take them, the rest is one skipped branch rather than a
+    // compare per case.
+    if (cem == 8 || cem == 12) {
+        const int a0 = cem == 12 ? v[6] : 255, a1 = cem == 12 ? v[7] : 255;
+        if (v[1] + v[3] + v[5] >= v[0] + v[2] + v[4]) {
+            e0[0] = v[0]; e0[1] = v[2]; e0[2] = v[4]; e0[3] = a0;
+            e1[0] = v[1]; e1[1] = v[3]; e1[2] = v[5]; e1[3] = a1;
+        } else {
+            // Swapped endpoints with blue contraction.
+            e0[0] = (v[1] + v[5]) >> 1; e0[1] = (v[3] + v[5]) >> 1; e0[2] = v[5]; e0[3] = a1;
+            e1[0] = (v[0] + v[4]) >> 1; e1[1] = (v[2] + v[4]) >> 1; e1[2] = v[4]; e1[3] = a0;
+        }
+        return true;
+    }
+    if (cem == 0) {
+        e0[0] = e0[1] = e0[2] = v[0]; e0[3] = 255;
+        e1[0] = e1[1] = e1[2] = v[1]; e1[3] = 255;
+        return true;
+    }
     switch (cem) {
-        case 0:
-            e0[0] = e0[1] = e0[2] = v[0]; e0[3] = 255;
-            e1[0] = e1[1] = e1[2] = v[1]; e1[3] = 255;
-            return true;
         case 1: {
             int l0 = (v[0] >> 2) | (v[1] & 0xC0);
             int l1 = min(l0 + (v[1] & 0x3F), 255);
@@ -417,19 +433,6 @@ __device__ inline bool cem_endpoints(int cem, const uint32_t* cv, int k, int* e0
             e0[3] = cem == 10 ? v[4] : 255;
             e1[0] = v[0]; e1[1] = v[1]; e1[2] = v[2];
             e1[3] = cem == 10 ? v[5] : 255;
-            return true;
-        }
-        case 8:
-        case 12: {
-            int a0 = cem == 12 ? v[6] : 255, a1 = cem == 12 ? v[7] : 255;
-            if (v[1] + v[3] + v[5] >= v[0] + v[2] + v[4]) {
-                e0[0] = v[0]; e0[1] = v[2]; e0[2] = v[4]; e0[3] = a0;
-                e1[0] = v[1]; e1[1] = v[3]; e1[2] = v[5]; e1[3] = a1;
-            } else {
-                // Swapped endpoints with blue contraction.
-                e0[0] = (v[1] + v[5]) >> 1; e0[1] = (v[3] + v[5]) >> 1; e0[2] = v[5]; e0[3] = a1;
-                e1[0] = (v[0] + v[4]) >> 1; e1[1] = (v[2] + v[4]) >> 1; e1[2] = v[4]; e1[3] = a0;
-            }
             return true;
         }
         case 9:
