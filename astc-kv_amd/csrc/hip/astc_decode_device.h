@@ -691,7 +691,8 @@ __device__ __attribute__((always_inline)) inline void decode_header(const LdsTab
         uint32_t ep[NCH];
         if (cem_endpoints(cem, cv, k, e0, e1)) {
 #pragma unroll
-            for (int ch = 0; ch < NCH; ++ch) ep[ch] = uint32_t(e0[ch] * 257) | (uint32_t(e1[ch] * 257) << 16);
+            for (int ch = 0; ch < NCH; ++ch)   // e * 257 = the byte twice (endpoints are 0..255)
+                ep[ch] = __builtin_amdgcn_perm(uint32_t(e1[ch]), uint32_t(e0[ch]), 0x04040000u);
         } else {
             const uint32_t err[4] = {0xFFFFFFFFu, 0u, 0xFFFFFFFFu, 0xFFFFFFFFu};
 #pragma unroll
