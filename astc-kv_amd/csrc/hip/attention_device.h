@@ -20,6 +20,7 @@ namespace akv_hip {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
+constexpr uint64_t kCUs = 256;   // compute units of an MI355X (gfx950)
 constexpr int kMaxG = 8;   // query heads per kv head
 #ifndef AKV_ASTC_WAVES
 #define AKV_ASTC_WAVES 3   // waves per SIMD the split kernel is register-limited to
@@ -28,11 +29,14 @@ constexpr int kMaxG = 8;   // query heads per kv head
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-template <int D, int NCH>
+// WIDE: the launch has at most one workgroup per CU (small batches, few
+// splits), so LDS has room for a full 256-block chunk at head dim 64 too:
+// fewer chunks, hence a shorter critical path, per split.
+template <int D, int NCH, bool WIDE = false>
 struct Cfg {
     // Blocks per chunk (header stage, one per lane): at head dim 128 the
     // kernel runs two workgroups per CU, which leaves room for a full 256.
-    static constexpr int kMaxBlocks = D == 64 ? 160 : 256;
+    static constexpr int kMaxBlocks = (D == 64 && !WIDE) ? 160 : 256;
     static constexpr int kMaxTok = D == 64 ? 320 : 128;          // tokens per chunk
     static constexpr int kMaxTiles = kMaxTok / 16;
     static constexpr int kWaveTiles = kMaxTiles / kWaves;        // tiles per wave per chunk
@@ -46,9 +50,10 @@ struct Cfg {
 struct KernelArgs {
     AkvAttnParams p;
     Footprint fp;
-    uint32_t chunk_tokens;   // tokens per full chunk (whole block rows for ASTC V)
+    uint32_t chunk_tokens;   // tokens per full chunk
     uint32_t mag_by, mag_bx; // ceil(2^24 / divisor)
     float qscale;            // log2(e) / sqrt(dim)
+    uint32_t wide;           // the split kernel's Cfg<..., WIDE = true> variant
 };
 
 // a / d with magic = ceil(2^24 / d): exact when a * d < 2^24 (the error term
@@ -528,9 +533,9 @@ __device__ inline void combine_waves(float* comb, WaveStats& ws, AttnState<D>& s
 
 // --- ASTC split kernel -------------------------------------------------------
 
-template <int D, int NCH>
+template <int D, int NCH, bool WIDE = false>
 struct AstcShared {
-    using C = Cfg<D, NCH>;
+    using C = Cfg<D, NCH, WIDE>;
     LdsTables tabs;
     union {
         struct {

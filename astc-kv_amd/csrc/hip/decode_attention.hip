@@ -39,18 +39,18 @@
 
 namespace akv_hip {
 
-template <int D, int NCH, int G, bool DUMP>
+template <int D, int NCH, int G, bool DUMP, bool WIDE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 64 ? AKV_ASTC_WAVES : 2))) void astc_attn_kernel(
     KernelArgs a, const float* __restrict__ q, const uint16_t* __restrict__ k, const uint4* __restrict__ vblk,
     const uint16_t* __restrict__ vscale, const uint16_t* __restrict__ voffset, const AkvTables* __restrict__ tab,
     float* partial, float2* stats, uint16_t* __restrict__ dump, float* __restrict__ out, uint32_t* arrivals) {
-    using C = Cfg<D, NCH>;
+    using C = Cfg<D, NCH, WIDE>;
     constexpr int TPG = Grp<G, D>::TPG;
     // K tiles of a wave's first group: the first kKEarly requested with the
     // chunk's other loads, the rest just before the header stage (all arrive
     // during it; issued together they stall the chunk's first phase).
     constexpr int kKEarly = TPG < 2 ? TPG : 2;
-    __shared__ AstcShared<D, NCH> sh;
+    __shared__ AstcShared<D, NCH, WIDE> sh;
     const AkvAttnParams& p = a.p;
     const Footprint f = a.fp;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -481,9 +481,9 @@ int check_astc(const AkvAttnParams* p) {
 // Chunk shape. ASTC V: the most whole block rows whose blocks fit the header
 // stage and whose tokens fit a chunk; FP16 control: a whole chunk. Never more
 // than one split.
-template <int D, int NCH>
+template <int D, int NCH, bool WIDE>
 int plan_chunks(const AkvAttnParams* p, bool astc, KernelArgs* a) {
-    using C = Cfg<D, NCH>;
+    using C = Cfg<D, NCH, WIDE>;
     uint32_t tokens = C::kMaxTok;
     if (astc) {
         // Chunks start on 16-token boundaries, at row offset c0 % by <= by -
@@ -520,8 +520,13 @@ int make_args(const AkvAttnParams* p, bool astc, KernelArgs* a) {
     }
     a->qscale = float(1.4426950408889634 / std::sqrt(double(p->dim)));
     const bool scalar = astc && p->layout == AKV_LAYOUT_SCALAR;
-    if (p->dim == 64) return scalar ? plan_chunks<64, 1>(p, astc, a) : plan_chunks<64, 4>(p, astc, a);
-    return scalar ? plan_chunks<128, 1>(p, astc, a) : plan_chunks<128, 4>(p, astc, a);
+    // At most one workgroup per CU (MI355X: 256 CUs): the wide split kernel.
+    a->wide = astc && p->dim == 64 && uint64_t(p->splits) * p->kv_heads * p->batch <= kCUs;
+    if (p->dim == 64) {
+        if (a->wide) return scalar ? plan_chunks<64, 1, true>(p, astc, a) : plan_chunks<64, 4, true>(p, astc, a);
+        return scalar ? plan_chunks<64, 1, false>(p, astc, a) : plan_chunks<64, 4, false>(p, astc, a);
+    }
+    return scalar ? plan_chunks<128, 1, false>(p, astc, a) : plan_chunks<128, 4, false>(p, astc, a);
 }
 
 struct Ptrs {
@@ -539,19 +544,19 @@ struct Ptrs {
     uint32_t* arrivals = nullptr;     // non-null: merge in the split kernel
 };
 
-template <int D, int NCH, bool DUMP>
+template <int D, int NCH, bool DUMP, bool WIDE>
 hipError_t launch_astc_g(const KernelArgs& a, uint32_t G, const Ptrs& x, hipStream_t st) {
     dim3 grid(a.p.splits, a.p.kv_heads, a.p.batch);
     auto* s2 = reinterpret_cast<float2*>(x.stats);
     if constexpr (DUMP) {
-        astc_attn_kernel<D, NCH, 1, true><<<grid, kThreads, 0, st>>>(a, x.q, x.k, x.vblk, x.vs, x.vo, x.tab, x.partial,
+        astc_attn_kernel<D, NCH, 1, true, WIDE><<<grid, kThreads, 0, st>>>(a, x.q, x.k, x.vblk, x.vs, x.vo, x.tab, x.partial,
                                                                       s2, x.dump, nullptr, nullptr);
         return hipGetLastError();
     }
     switch (G) {
 #define AKV_CASE(GG)                                                                                       \
     case GG:                                                                                               \
-        astc_attn_kernel<D, NCH, GG, DUMP><<<grid, kThreads, 0, st>>>(a, x.q, x.k, x.vblk, x.vs, x.vo, x.tab, \
+        astc_attn_kernel<D, NCH, GG, DUMP, WIDE><<<grid, kThreads, 0, st>>>(a, x.q, x.k, x.vblk, x.vs, x.vo, x.tab, \
                                                                        x.partial, s2, x.dump, x.out,      \
                                                                        x.arrivals);                       \
         break;
@@ -570,8 +575,12 @@ hipError_t launch_astc_g(const KernelArgs& a, uint32_t G, const Ptrs& x, hipStre
 template <bool DUMP>
 hipError_t launch_astc(const KernelArgs& a, uint32_t G, const Ptrs& x, hipStream_t st) {
     const bool scalar = a.p.layout == AKV_LAYOUT_SCALAR;
-    if (a.p.dim == 64) return scalar ? launch_astc_g<64, 1, DUMP>(a, G, x, st) : launch_astc_g<64, 4, DUMP>(a, G, x, st);
-    return scalar ? launch_astc_g<128, 1, DUMP>(a, G, x, st) : launch_astc_g<128, 4, DUMP>(a, G, x, st);
+    if (a.p.dim == 64) {
+        if (a.wide)
+            return scalar ? launch_astc_g<64, 1, DUMP, true>(a, G, x, st) : launch_astc_g<64, 4, DUMP, true>(a, G, x, st);
+        return scalar ? launch_astc_g<64, 1, DUMP, false>(a, G, x, st) : launch_astc_g<64, 4, DUMP, false>(a, G, x, st);
+    }
+    return scalar ? launch_astc_g<128, 1, DUMP, false>(a, G, x, st) : launch_astc_g<128, 4, DUMP, false>(a, G, x, st);
 }
 
 template <int D>

@@ -53,19 +53,31 @@ def c3(**kw):
 
 
 def test_chunk_tokens_follow_the_footprint(hip):
-    # 6x5 RGBA D64: 3 block columns, at most 160 blocks -> 53 block rows; a
-    # chunk starts on a 16-token boundary, at most 4 tokens into its first
-    # row, so 261 tokens fit; 256 = 16 tiles, the same number for every wave.
-    assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=8192, splits=1)), 1) == 256
+    # Launches of more workgroups than CUs (16 splits x 3 kv heads x batch 16
+    # = 768): at head dim 64 a chunk holds at most 160 blocks.
+    big = dict(tile_tokens=512, splits=16)
+    # 6x5 RGBA D64: 3 block columns -> 53 block rows; a chunk starts on a
+    # 16-token boundary, at most 4 tokens into its first row, so 261 tokens
+    # fit; 256 = 16 tiles, the same number for every wave.
+    assert hip.akv_hip_task_tokens(ct.byref(c3(**big)), 1) == 256
     # A split shorter than a chunk is one chunk.
     assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=48, splits=171)), 1) == 48
     # 4x4 RGBA D64: 4 block columns -> 40 block rows = 160 tokens.
-    p = c3(block_x=4, block_y=4, atlas_cols=4, atlas_rows=2048, tile_tokens=8192, splits=1)
+    p = c3(block_x=4, block_y=4, atlas_cols=4, atlas_rows=2048, **big)
     assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 160
     # Scalar 6x6 D64: 11 block columns -> 14 rows = 84 tokens, at most 4 in
     # at the start -> 80.
-    p = c3(layout=0, block_x=6, block_y=6, atlas_cols=11, atlas_rows=1366, tile_tokens=8192, splits=1)
+    p = c3(layout=0, block_x=6, block_y=6, atlas_cols=11, atlas_rows=1366, **big)
     assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 80
+    # At most one workgroup per CU (1 split x 48): the wide kernel's 256-block
+    # chunks. 6x5: 85 rows, capped at 320 tokens -> 256; 4x4: 64 rows = 256;
+    # scalar 6x6: 23 rows = 138 tokens, 4 in at the start -> 128.
+    one = dict(tile_tokens=8192, splits=1)
+    assert hip.akv_hip_task_tokens(ct.byref(c3(**one)), 1) == 256
+    p = c3(block_x=4, block_y=4, atlas_cols=4, atlas_rows=2048, **one)
+    assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 256
+    p = c3(layout=0, block_x=6, block_y=6, atlas_cols=11, atlas_rows=1366, **one)
+    assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 128
     # D128 RGBA 4x4: 8 block columns, at most 256 blocks -> 32 rows = 128 tokens.
     p = c3(dim=128, block_x=4, block_y=4, atlas_cols=8, atlas_rows=2048, tile_tokens=8192, splits=1)
     assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 128
