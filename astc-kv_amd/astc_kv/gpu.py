@@ -114,7 +114,10 @@ def default_tile(batch: int, kv_heads: int, tokens: int, chunk: int, block: int 
     """Tokens per split (a multiple of `block`: 16 for the kernels here).
 
     * Fewer chunks than CUs: splits of about tokens * batch * kv_heads / CUs
-      tokens (at least 16) for parallelism.
+      tokens (at least 16) for parallelism, but at most 24 splits per
+      sequence (the merge reads every split's state: T2048 batch 1 runs in
+      19 us with 64 splits, 16.6 us with 16, 13.3 us for T384 with 24);
+      above 64 tokens, whole groups of four tiles (multiples of 64).
     * Up to 8 rounds of resident workgroups (groups_per_cu per CU): the tile
       (at most 8 chunks) minimising rounds x (tile + overhead_tokens), i.e.
       the time of the last workgroup to finish when each costs its tokens plus
@@ -126,8 +129,9 @@ def default_tile(batch: int, kv_heads: int, tokens: int, chunk: int, block: int 
     slots = groups_per_cu * cu_count
     total = seqs * -(-tokens // chunk)
     if total < cu_count:
-        want = max(16, -(-tokens * seqs // cu_count))
-        return min(chunk, -(-want // block) * block)
+        want = max(16, -(-tokens * seqs // cu_count), -(-tokens // 24))
+        step = 64 if want > 64 else block
+        return min(chunk, -(-want // step) * step)
     if total <= 8 * slots:
         top = min(8 * chunk, -(-tokens // block) * block)
         tiles = range(top - top % block, 0, -block)
