@@ -220,6 +220,14 @@ def _counter_means(directory: str, counter: str):
     return {k: sums[k] / counts[k] for k in sums}
 
 
+def _is_split_kernel(name: str) -> bool:
+    """astc_attn_kernel<D, NCH, G, DUMP, WIDE> with DUMP false (not the decode readback)."""
+    if not name.startswith("astc_attn_kernel<"):
+        return False
+    args = [x.strip() for x in name[name.index("<") + 1:name.rindex(">")].split(",")]
+    return len(args) >= 4 and args[3] == "false"
+
+
 def summarize_counters(dirs, kernels=("astc_attn_kernel", "fp16_attn_kernel")) -> str:
     """Markdown table of every PMC counter found under `dirs` (rocprofv3
     --pmc output), mean per dispatch, for the kernels whose names start with
@@ -258,7 +266,7 @@ def summarize(kt_dir: str, fetch_dir: str, write_dir: str, calib_mb: float, work
                    f"{fetch.get(name, float('nan')):.1f} | {write.get(name, float('nan')):.1f} |")
     text = "\n".join(out) + "\n"
     copy = [k for k in fetch if COPY_KERNEL in k]
-    split = [k for k in fetch if k.startswith("astc_attn_kernel") and ", false>" in k]
+    split = [k for k in fetch if _is_split_kernel(k)]
     if copy and calib_mb > 0:
         nbytes = calib_mb * 1e6
         ff = nbytes / (fetch[copy[0]] * 1024)
