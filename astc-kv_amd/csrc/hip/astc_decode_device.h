@@ -53,6 +53,7 @@ static_assert(offsetof(LdsTables, color_unq) == offsetof(AkvTables, color_unq) &
                   offsetof(LdsTables, weight_unq) == offsetof(AkvTables, weight_unq) &&
                   offsetof(LdsTables, weight_levels) == offsetof(AkvTables, weight_levels),
               "LdsTables field offsets");
+static_assert(offsetof(LdsTables, weight_unq) % 4 == 0, "weight rows are read a dword at a time");
 
 // BlockDesc.info fields (bits 0-3 grid width, 4-7 grid height).
 constexpr uint32_t kInfoDual = 1u << 8;         // bits 9-10: colour component of plane 1
@@ -467,17 +468,24 @@ __device__ inline bool cem_endpoints(int cem, const uint32_t* cv, int k, int* e0
 // 0x10000, so that C' / 65536 rounded toward zero is the FP16 value astcenc
 // returns. With y = dot + 96 = (C + 1) * 64 + r (0 <= r < 64),
 // C' = (y >> 6) + (y >> 22) - 1.
+//
+// C' is carried biased, as the bits of the float 128 + C' / 65536 (C' in the
+// mantissa of 2^7, whose ulp is 2^-16; C' <= 0x10000 < 2^23): the bias folds
+// into the add, and one exact subtraction of 128 (Sterbenz) replaces an
+// integer-to-float conversion and a scale.
+constexpr uint32_t kCBias = 0x43000000u;   // bits of 128.0f
+
 __device__ inline uint32_t interp_c(uint32_t ep, uint32_t wp) {
     typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
     const uint32_t y =
         __builtin_amdgcn_udot2(__builtin_bit_cast(u16x2, ep), __builtin_bit_cast(u16x2, wp), 96u, false);
-    return (y >> 6) + (y >> 22) - 1u;
+    return (y >> 6) + (y >> 22) + (kCBias - 1u);
 }
 
-// Two C' values -> their FP16 values (round toward zero), packed.
+// Two biased C' values -> their FP16 values (round toward zero), packed.
 __device__ inline uint32_t pack_fp16_rtz(uint32_t c0, uint32_t c1) {
-    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(float(c0) * (1.0f / 65536.0f),
-                                                                   float(c1) * (1.0f / 65536.0f)));
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__builtin_bit_cast(float, c0) - 128.0f,
+                                                                   __builtin_bit_cast(float, c1) - 128.0f));
 }
 
 __device__ inline uint32_t weight_pair(int w) { return uint32_t(64 - w) | (uint32_t(w) << 16); }
@@ -490,7 +498,7 @@ __device__ inline void put_entry(uint32_t* tab, int entry, const uint32_t* ep, u
         tab[2 * entry] = pack_fp16_rtz(interp_c(ep[0], wp), interp_c(ep[1], wp));
         tab[2 * entry + 1] = pack_fp16_rtz(interp_c(ep[2], wp), interp_c(ep[3], wp));
     } else {
-        reinterpret_cast<uint16_t*>(tab)[entry] = uint16_t(pack_fp16_rtz(interp_c(ep[0], wp), 0));
+        reinterpret_cast<uint16_t*>(tab)[entry] = uint16_t(pack_fp16_rtz(interp_c(ep[0], wp), kCBias));
     }
 }
 
@@ -503,13 +511,13 @@ __device__ inline void put_end_entry(uint32_t* tab, int entry, const uint32_t* e
 #pragma unroll
     for (int ch = 0; ch < NCH; ++ch) {
         const uint32_t e = (ep[ch] >> sh) & 0xFFFFu;
-        C[ch] = e + ((e + 1) >> 16);
+        C[ch] = e + ((e + 1) >> 16) + kCBias;
     }
     if constexpr (NCH == 4) {
         tab[2 * entry] = pack_fp16_rtz(C[0], C[1]);
         tab[2 * entry + 1] = pack_fp16_rtz(C[2], C[3]);
     } else {
-        reinterpret_cast<uint16_t*>(tab)[entry] = uint16_t(pack_fp16_rtz(C[0], 0));
+        reinterpret_cast<uint16_t*>(tab)[entry] = uint16_t(pack_fp16_rtz(C[0], kCBias));
     }
 }
 
@@ -685,6 +693,10 @@ __device__ __attribute__((always_inline)) inline void decode_header(const LdsTab
     const int levels = L.weight_levels[wrange];
     const bool identity = akv::mode_identity(md);
     const bool table = identity && !dual && parts * levels <= BlockDesc<NCH>::kTabEntries;
+    // Unquantised weights of the first 8 fields (all an RGBA table row can
+    // hold), one LDS read rather than one per entry.
+    const uint32_t* wrow_words = reinterpret_cast<const uint32_t*>(&L.weight_unq[wrange][0]);
+    const uint2 wrow = {wrow_words[0], wrow_words[1]};
     for (int p = 0, k = 0; p < parts; ++p) {
         const int cem = int((cems >> (4 * p)) & 15);
         int e0[4], e1[4];
@@ -708,7 +720,9 @@ __device__ __attribute__((always_inline)) inline void decode_header(const LdsTab
 #pragma unroll
             for (int q = 1; q < BlockDesc<NCH>::kTabEntries; ++q) {
                 if (q >= levels) break;
-                put_entry<NCH>(d.tab, p * levels + q, ep, weight_pair(L.weight_unq[wrange][q]));
+                const int w = q < 8 ? int(((q < 4 ? wrow.x : wrow.y) >> (8 * (q & 3))) & 0xFFu)
+                                    : int(L.weight_unq[wrange][q]);
+                put_entry<NCH>(d.tab, p * levels + q, ep, weight_pair(w));
             }
         } else {
 #pragma unroll
@@ -763,7 +777,7 @@ __device__ __attribute__((noinline)) uint2 texel_compute(const BlockDesc<NCH>& d
 #pragma unroll
     for (int ch = 0; ch < NCH; ++ch) C[ch] = interp_c(d.ep[p][ch], ch == ccs ? wp1 : wp0);
     if constexpr (NCH == 4) return uint2{pack_fp16_rtz(C[0], C[1]), pack_fp16_rtz(C[2], C[3])};
-    else return uint2{pack_fp16_rtz(C[0], 0) & 0xFFFFu, 0u};
+    else return uint2{pack_fp16_rtz(C[0], kCBias) & 0xFFFFu, 0u};
 }
 
 // Stage 2: the FP16 values of texel (x, y) of a block (NCH == 4:
