@@ -780,6 +780,22 @@ __device__ __attribute__((noinline)) uint2 texel_compute(const BlockDesc<NCH>& d
     else return uint2{pack_fp16_rtz(C[0], kCBias) & 0xFFFFu, 0u};
 }
 
+// Stage 2, compute path of a block with one weight plane and a weight grid
+// the size of the block (texel i reads weight field i): inlined for RGBA,
+// since at RGBA 4x4 most blocks (two partitions, 5-10 weight levels) have
+// more entries than a table holds and take this path. (A scalar table holds
+// 32 entries, so scalar blocks rarely miss it.)
+template <int NCH>
+__device__ inline uint2 texel_identity(const BlockDesc<NCH>& d, const LdsTables& L, uint32_t info, int i, int p) {
+    const uint32_t nb = (info >> kInfoNbShift) & 7;
+    const uint32_t wp = weight_pair(L.weight_unq[(info >> kInfoRangeShift) & 15][field_at(d, nb, i)]);
+    uint32_t C[NCH];
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) C[ch] = interp_c(d.ep[p][ch], wp);
+    if constexpr (NCH == 4) return uint2{pack_fp16_rtz(C[0], C[1]), pack_fp16_rtz(C[2], C[3])};
+    else return uint2{pack_fp16_rtz(C[0], kCBias) & 0xFFFFu, 0u};
+}
+
 // Stage 2: the FP16 values of texel (x, y) of a block (NCH == 4:
 // {R | G << 16, B | A << 16}; NCH == 1: R in the low half of .x).
 template <int NCH>
@@ -825,8 +841,12 @@ __device__ inline void texels_fp16(const BlockDesc<NCH>* desc, const int (&blk)[
     if (!all_table) {
 #pragma unroll
         for (int k = 0; k < K; ++k)
-            if (!(info[k] & kInfoTable))
-                out[k] = texel_compute<NCH>(desc[blk[k]], L, f.bx, f.ds, f.dt, x[k], y[k], p[k]);
+            if (!(info[k] & kInfoTable)) {
+                if (NCH == 4 && (info[k] & (kInfoIdentity | kInfoDual)) == kInfoIdentity)
+                    out[k] = texel_identity<NCH>(desc[blk[k]], L, info[k], i[k], p[k]);
+                else
+                    out[k] = texel_compute<NCH>(desc[blk[k]], L, f.bx, f.ds, f.dt, x[k], y[k], p[k]);
+            }
     }
 }
 
