@@ -42,7 +42,7 @@ for _p in (ROOT, ROOT / "astc-kv_amd"):
         sys.path.insert(0, str(_p))
 
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_FILE = ROOT / "profiles" / "astc_split_kernel_T8192_b16_rgba6x5.md"
+PROFILES = ROOT / "profiles"
 COPY_KERNEL = "neg_kernel"   # the calibration copy: torch.neg over float32 (reads N bytes, writes N bytes)
 
 
@@ -72,7 +72,9 @@ def parse_args(argv=None):
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--copy-calibration-mb", type=float, default=0.0,
                     help="also run a plain copy kernel over this many MB (for rocprofv3 counter scaling)")
-    ap.add_argument("--traffic", default=str(TRAFFIC_FILE), help="profile summary holding the measured traffic")
+    ap.add_argument("--traffic", default=None,
+                    help="profile summary holding the measured traffic (default: the summary under profiles/ "
+                         "whose workload line names this workload)")
     ap.add_argument("--counters", nargs="+", metavar="PMC_DIR",
                     help="print a table of the PMC counters in these rocprofv3 --pmc output directories")
     ap.add_argument("--summarize", nargs=3, metavar=("KT", "FETCH", "WRITE"),
@@ -184,8 +186,15 @@ def cpu_baseline(q, k, v_restored, seconds):
     return res[cores][0], cores, res[1][0], res[cores][1]
 
 
-def read_traffic(path: str, workload: str):
-    """Traffic per split launch from a profile summary whose `workload:` line matches."""
+def read_traffic(path, workload: str):
+    """Traffic per split launch from a profile summary whose `workload:` line
+    matches; with no path, the first such summary under profiles/."""
+    if path is None:
+        for cand in sorted(PROFILES.glob("*.md")):
+            got = read_traffic(str(cand), workload)
+            if got:
+                return got
+        return None
     p = Path(path)
     if not p.exists():
         return None
