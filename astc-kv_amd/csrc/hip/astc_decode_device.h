@@ -827,7 +827,8 @@ __device__ inline void texels_fp16(const BlockDesc<NCH>* desc, const int (&blk)[
 #pragma unroll
     for (int k = 0; k < K; ++k) {
         info[k] = desc[blk[k]].info;
-        p[k] = int(__builtin_amdgcn_ubfe(desc[blk[k]].part[i[k] >> 4], 2 * (i[k] & 15), 2));
+        // v_bfe_u32 reads its offset mod 32: 2 * i selects bits 2 * (i % 16).
+        p[k] = int(__builtin_amdgcn_ubfe(desc[blk[k]].part[i[k] >> 4], uint32_t(2 * i[k]), 2));
     }
 #pragma unroll
     for (int k = 0; k < K; ++k) {
