@@ -207,13 +207,29 @@ constexpr int ise_max_values(int r, int cap, int budget) {
 // emit(Idx<j>, value) with value = digit << bits | plain bits. Values past the
 // real sequence are garbage (bits past its end must already be zero, since a
 // truncated trit/quint group decodes with its missing bits as zero).
+// vlim (wave-uniform): the trit/quint groups that hold only values vlim and
+// up are skipped, at two branch points (past 16 and past 36 values), so that
+// the groups below stay straight-line code. A vlim the compiler knows to be
+// >= the value count removes the branches.
+template <int GS, int NG, typename Group>
+__device__ __attribute__((always_inline)) inline void ise_groups(int vlim, Group&& group) {
+    constexpr int G16 = NG < (16 + GS - 1) / GS ? NG : (16 + GS - 1) / GS;
+    constexpr int G36 = NG < (36 + GS - 1) / GS ? NG : (36 + GS - 1) / GS;
+    static_for<0, G16>(group);
+    if (vlim > 16) {
+        static_for<G16, G36>(group);
+        if (vlim > 36) static_for<G36, NG>(group);
+    }
+}
+
 template <int R, int V, typename Emit>
-__device__ __attribute__((always_inline)) inline void ise_unpack(const uint32_t (&s)[4], const LdsTables& L, Emit&& emit) {
+__device__ __attribute__((always_inline)) inline void ise_unpack(const uint32_t (&s)[4], const LdsTables& L, int vlim,
+                                                                 Emit&& emit) {
     constexpr akv::IseRange e = akv::kIse[R];
     constexpr int n = e.bits;
     if constexpr (e.trit) {
         constexpr int gb = 5 * n + 8;
-        static_for<0, (V + 4) / 5>([&](auto gi) {
+        ise_groups<5, (V + 4) / 5>(vlim, [&](auto gi) {
             constexpr int p = decltype(gi)::value * gb;
             uint32_t T;
             if constexpr (n == 0) {
@@ -232,7 +248,7 @@ __device__ __attribute__((always_inline)) inline void ise_unpack(const uint32_t 
         });
     } else if constexpr (e.quint) {
         constexpr int gb = 3 * n + 7;
-        static_for<0, (V + 2) / 3>([&](auto gi) {
+        ise_groups<3, (V + 2) / 3>(vlim, [&](auto gi) {
             constexpr int p = decltype(gi)::value * gb;
             uint32_t Q;
             if constexpr (n == 0) {
@@ -262,7 +278,7 @@ __device__ __attribute__((always_inline)) inline void colour_values(const uint32
                                                                     uint32_t* cv) {
     constexpr int V = ise_max_values(R, 18, 111);
     uint32_t w[(V + 3) / 4] = {};
-    ise_unpack<R, V>(s, L, [&](auto ji, uint32_t v) {
+    ise_unpack<R, V>(s, L, 64, [&](auto ji, uint32_t v) {
         constexpr int j = decltype(ji)::value;
         w[j / 4] |= uint32_t(L.color_unq[R][v]) << (8 * (j % 4));
     });
@@ -273,16 +289,17 @@ __device__ __attribute__((always_inline)) inline void colour_values(const uint32
 // Weight fields of trit/quint range R as plain nb-bit fields (nb = bits + 2
 // for trits, bits + 3 for quints), field j at bit j * nb of q (five words).
 // At most 64 weights, never more than fit in 96 bits.
+// vlim: as ise_unpack's (at least the block's weight count).
 template <int R>
 __device__ __attribute__((always_inline)) inline void weight_fields(const uint32_t (&s)[4], const LdsTables& L,
-                                                                    uint32_t (&q)[5]) {
+                                                                    uint32_t (&q)[5], int vlim) {
     constexpr akv::IseRange e = akv::kIse[R];
     constexpr int nb = e.bits + (e.trit ? 2 : 3);
     constexpr int V = ise_max_values(R, 64, 96);
     static_assert(V * nb <= 160, "weight fields fit five words");
 #pragma unroll
     for (int i = 0; i < 5; ++i) q[i] = 0;
-    ise_unpack<R, V>(s, L, [&](auto ji, uint32_t v) {
+    ise_unpack<R, V>(s, L, vlim, [&](auto ji, uint32_t v) {
         constexpr int P = decltype(ji)::value * nb, w = P >> 5, o = P & 31;
         q[w] |= v << o;
         if constexpr (o + nb > 32) q[w + 1] |= v >> (32 - o);
@@ -328,19 +345,29 @@ __device__ __attribute__((always_inline)) inline void decode_colour_values(const
 }
 
 // Weight integer sequence of this lane's block (range `wrange`, `wbits` bits
-// of the bit-reversed block `rev`) -> nb-bit fields in q. Plain ranges are
-// already nb-bit fields.
-__device__ __attribute__((always_inline)) inline void decode_weight_fields(const uint32_t* rev, int wrange, int wbits, const LdsTables& L,
-                                            uint32_t (&q)[5]) {
+// of the bit-reversed block `rev`, `count` weights) -> nb-bit fields in q.
+// Plain ranges are already nb-bit fields. With CAP, a wave takes one pass
+// per distinct (range, cap of the weight count: 16, 36 or 64), the blocks of
+// one class sharing both, and decodes only the trit/quint groups below the
+// cap (4x4 grids: 16 values rather than up to 41). The uniform branches cost
+// about 13 registers: the D=64 kernels (which would spill) and the paged
+// kernel (measured slower) decode every value that fits.
+template <bool CAP>
+__device__ __attribute__((always_inline)) inline void decode_weight_fields(const uint32_t* rev, int wrange, int wbits,
+                                                                           int count, const LdsTables& L,
+                                                                           uint32_t (&q)[5]) {
     const uint4 r4 = *reinterpret_cast<const uint4*>(rev);
+    const int key = CAP ? (wrange | ((count <= 16 ? 0 : count <= 36 ? 1 : 2) << 4)) : wrange;
     while (true) {
-        const int r = __builtin_amdgcn_readfirstlane(wrange);
-        if (wrange == r) {
+        const int rk = __builtin_amdgcn_readfirstlane(key);
+        if (key == rk) {
             uint32_t s[4] = {r4.x, r4.y, r4.z, r4.w};
+            const int r = CAP ? (rk & 15) : rk;
+            const int vlim = CAP ? ((rk >> 4) == 0 ? 16 : ((rk >> 4) == 1 ? 36 : 64)) : 64;
             auto run = [&](auto ri) {
                 constexpr int R = decltype(ri)::value;
                 shift_and_cut(s, 0u, wbits);
-                weight_fields<R>(s, L, q);
+                weight_fields<R>(s, L, q, vlim);
             };
             switch (r) {
                 case 1: run(Idx<1>{}); break;
@@ -611,7 +638,7 @@ __device__ inline uint4 block_part_words(uint4 raw, uint4 words) {
 // `cv` is this lane's scratch for the unquantised colour values
 // (kColourScratchWords dwords, four values per dword).
 // Every table read is from LDS.
-template <int NCH>
+template <int NCH, bool CAP = false>
 __device__ __attribute__((always_inline)) inline void decode_header(const LdsTables& L, BlockDesc<NCH>& d,
                                                                    uint32_t* cv) {
     const uint32_t* blk = d.tab;        // block bits
@@ -683,7 +710,8 @@ __device__ __attribute__((always_inline)) inline void decode_header(const LdsTab
     const int nb = int(wi & 0xFF) + ((wi & 0x100) ? 2 : (wi & 0x200) ? 3 : 0);
     {
         uint32_t q[5];
-        decode_weight_fields(rev, wrange, wbits, L, q);
+        const int count = int(akv::mode_gw(md) * akv::mode_gh(md)) << (dual ? 1 : 0);
+        decode_weight_fields<CAP>(rev, wrange, wbits, count, L, q);
 #pragma unroll
         for (int i = 0; i < 5; ++i) d.qw[i] = q[i];
     }

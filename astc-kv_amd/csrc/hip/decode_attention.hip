@@ -157,7 +157,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
             for (int t = kKEarly; t < TPG; ++t)
                 load_k_tile<D>(kreg + t * C::kRowLoads, krs, 16 * (TPG * wave + t), lane);
         }
-        if (tid < nblk) decode_header<NCH>(sh.tabs, sh.u.h.desc[sh.order[tid]], sh.u.h.cv[tid]);
+        if (tid < nblk) decode_header<NCH, D == 128>(sh.tabs, sh.u.h.desc[sh.order[tid]], sh.u.h.cv[tid]);
         // What the texel stage needs besides the headers: each lane's own
         // block's partition words, and the per-token scale | offset << 16
         // (zero past the chunk, up to the tile edge).
