@@ -118,13 +118,15 @@ def default_tile(batch: int, kv_heads: int, tokens: int, chunk: int, block: int 
       sequence (the merge reads every split's state: T2048 batch 1 runs in
       19 us with 64 splits, 16.6 us with 16, 13.3 us for T384 with 24);
       above 64 tokens, whole groups of four tiles (multiples of 64).
-    * Up to 8 rounds of resident workgroups (groups_per_cu per CU): the tile
-      (at most 8 chunks) minimising rounds x (tile + overhead_tokens), i.e.
-      the time of the last workgroup to finish when each costs its tokens plus
-      a fixed overhead (a partial last round idles most CUs); among tiles
+    * Up to 32 rounds of one-chunk workgroups (groups_per_cu per CU): the
+      tile (at most 16 chunks) minimising rounds x (tile + overhead_tokens),
+      i.e. the time of the last workgroup to finish when each costs its tokens
+      plus a fixed overhead (a partial last round idles most CUs); among tiles
       within 3% of that minimum, the fewest splits, then the lowest cost.
-    * More: several chunks per split (up to 8), which also cuts the
-      split-state traffic; the tail is small there."""
+      (T32768 batch 8, 8 KV heads, D128: 16 chunks of 128 per split, two
+      rounds, 397 us; 8 chunks, four rounds, 407 us.)
+    * More: several chunks per split (up to 16, about two rounds or more),
+      which also cuts the split-state traffic; the tail is small there."""
     seqs = batch * kv_heads
     slots = groups_per_cu * cu_count
     total = seqs * -(-tokens // chunk)
@@ -132,8 +134,8 @@ def default_tile(batch: int, kv_heads: int, tokens: int, chunk: int, block: int 
         want = max(16, -(-tokens * seqs // cu_count), -(-tokens // 24))
         step = 64 if want > 64 else block
         return min(chunk, -(-want // step) * step)
-    if total <= 8 * slots:
-        top = min(8 * chunk, -(-tokens // block) * block)
+    if total <= 32 * slots:
+        top = min(16 * chunk, -(-tokens // block) * block)
         tiles = range(top - top % block, 0, -block)
         cost = {t: -(-seqs * -(-tokens // t) // slots) * (t + overhead_tokens) for t in tiles}
         floor = min(cost.values())
@@ -142,7 +144,7 @@ def default_tile(batch: int, kv_heads: int, tokens: int, chunk: int, block: int 
         near = [t for t in tiles if cost[t] <= 1.03 * floor]
         fewest = min(-(-tokens // t) for t in near)
         return min((cost[t], -t) for t in near if -(-tokens // t) == fewest)[1] * -1
-    per_split = max(1, min(8, total // (4 * slots)))
+    per_split = max(1, min(16, total // (2 * slots)))
     return per_split * chunk
 
 

@@ -228,9 +228,14 @@ def test_default_tiles():
     # 4x4 (160-token chunks): one full round of 16 splits.
     t = default_tile(16, 3, 8192, 160, 16)
     assert t % 16 == 0 and t == 512 and 48 * -(-8192 // t) == 768
-    # c4 (64 pairs, 80-token chunks, > 8 rounds): several chunks per split.
+    # 64 pairs of 32768 tokens in 80-token chunks (> 32 rounds): several
+    # chunks per split.
     t = default_tile(8, 8, 32768, 80, 4)
-    assert t % 80 == 0 and 80 < t <= 8 * 80
+    assert t % 80 == 0 and 80 < t <= 16 * 80
+    # c4 (64 pairs, 128-token chunks, two workgroups per CU): 16 splits of
+    # 2048 tokens, two full rounds on 256 CUs.
+    t = default_tile(8, 8, 32768, 128, 16, groups_per_cu=2)
+    assert t == 2048 and 64 * -(-32768 // t) == 2 * 512
     # Tiny workloads: split for parallelism, in whole tiles, never above a
     # chunk, at most 24 splits per sequence.
     t = default_tile(1, 3, 384, 256, 16)
