@@ -79,7 +79,13 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
     const Footprint f = a.fp;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int n16 = lane & 15, g = lane >> 4;
-    const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+    // Grid (kv head, sequence, split): workgroups are dispatched to the XCDs
+    // round robin in linear order, and with the split slowest every XCD gets
+    // an equal share of each split index. (With the split fastest and a
+    // power-of-two split count, split s of every sequence lands on XCD s % 8,
+    // and in a ragged batch the XCDs holding the late splits of only the
+    // long sequences idle while the others work: up to 2x slower.)
+    const int kh = blockIdx.x, b = blockIdx.y, split = blockIdx.z;
     const int len = lens[b];
     const int P = int(p.page_tokens);
     const int split_begin = split * int(p.tile_tokens);
@@ -405,7 +411,7 @@ int check_paged(const AkvPagedParams* p, uint32_t* G) {
     if (uint64_t(p->max_pages) * P < p->max_tokens) return AKV_HIP_ERR_SHAPE;
     const uint32_t T = p->tile_tokens;
     if (T == 0 || T % 16 || T % by) return AKV_HIP_ERR_TILE;
-    if (p->splits != (p->max_tokens + T - 1) / T || p->splits > 2147483647u) return AKV_HIP_ERR_TILE;
+    if (p->splits != (p->max_tokens + T - 1) / T || p->splits > 65535) return AKV_HIP_ERR_TILE;   // grid z
     // Pages a split touches; split-relative offsets times the divisors fit 24 bits.
     if ((T + P - 1) / P + 1 > uint32_t(kMaxSplitPages) || uint64_t(T + P) * P >= (1u << 24))
         return AKV_HIP_ERR_TILE;
@@ -465,7 +471,7 @@ struct PagedPtrs {
 
 template <int D, int NCH, bool KU4>
 hipError_t launch_paged_g(const PagedArgs& a, uint32_t G, const PagedPtrs& x, hipStream_t st) {
-    dim3 grid(a.p.splits, a.p.kv_heads, a.p.batch);
+    dim3 grid(a.p.kv_heads, a.p.batch, a.p.splits);
     switch (G) {
 #define AKV_CASE(GG)                                                                                          \
     case GG:                                                                                                  \

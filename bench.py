@@ -320,7 +320,7 @@ def main_ragged(a, torch, gpu):
     cache = gpu.DevicePagedKV.from_host(pk)
     q = rng.normal(size=(a.ragged, a.query_heads, a.dim)).astype(np.float32)
     qt = torch.from_numpy(q).cuda()
-    params = gpu.paged_params(cache, a.query_heads)
+    params = gpu.paged_params(cache, a.query_heads, a.tile or None)
     s = params.splits
     partial = torch.empty((a.ragged, a.query_heads, s, a.dim), dtype=torch.float32, device="cuda")
     stats = torch.empty((a.ragged, a.query_heads, s, 2), dtype=torch.float32, device="cuda")

@@ -168,7 +168,7 @@ typedef struct AkvPagedParams {
     uint32_t max_pages;     /* block_table row length, >= ceil(max_tokens / page_tokens) */
     uint32_t num_pages;     /* pages in each pool */
     uint32_t tile_tokens;   /* tokens per split: a multiple of 16 and of block_y */
-    uint32_t splits;        /* ceil(max_tokens / tile_tokens) */
+    uint32_t splits;        /* ceil(max_tokens / tile_tokens), at most 65535 */
     uint32_t layout;        /* AKV_LAYOUT_SCALAR or AKV_LAYOUT_RGBA */
     uint32_t block_x;
     uint32_t block_y;
