@@ -423,10 +423,11 @@ class DevicePagedKV:
 
 
 def paged_params(cache: DevicePagedKV, query_heads: int, tile: int | None = None, cu_count: int = 256) -> AkvPagedParams:
-    """Tile default: about six rounds of resident workgroups over the whole
+    """Tile default: about twelve rounds of resident workgroups over the whole
     ragged batch (in steps of lcm(16, block_y) tokens; with uneven lengths
     shorter splits balance the rounds), within the kernel's limit of 62 pages
-    per split."""
+    per split. (64 sequences of U[512,16384] tokens, 8 KV heads, D128: 720
+    tokens, 2.39 ms; six rounds, 1392 tokens: 2.46 ms.)"""
     P, by = cache.page_tokens, cache.block_y
     step = 16
     while step % by:
@@ -434,7 +435,7 @@ def paged_params(cache: DevicePagedKV, query_heads: int, tile: int | None = None
     max_t = max(cache.lens)
     if tile is None:
         groups = (3 if cache.dim == 64 else 2) * cu_count
-        want = -(-sum(cache.lens) * cache.kv_heads // (6 * groups))
+        want = -(-sum(cache.lens) * cache.kv_heads // (12 * groups))
         tile = max(step, -(-want // step) * step)
         limit = (62 * P) // step * step
         while (tile + P) * P >= 1 << 24:
