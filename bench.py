@@ -213,7 +213,7 @@ def read_traffic(path, workload: str):
 # --- rocprofv3 summary ----------------------------------------------------------------
 
 def _short(name: str) -> str:
-    name = name.replace("akv_hip::", "").replace("void ", "")
+    name = name.replace("akv_hip::", "").replace("(anonymous namespace)::", "").replace("void ", "")
     return name[: name.index("(")] if "(" in name else name
 
 
@@ -230,7 +230,10 @@ def _counter_means(directory: str, counter: str):
 
 
 def _is_split_kernel(name: str) -> bool:
-    """astc_attn_kernel<D, NCH, G, DUMP, WIDE> with DUMP false (not the decode readback)."""
+    """astc_attn_kernel<D, NCH, G, DUMP, WIDE> with DUMP false (not the decode
+    readback), or the paged kernel paged_attn_kernel<D, NCH, G, KU4>."""
+    if name.startswith("paged_attn_kernel<"):
+        return True
     if not name.startswith("astc_attn_kernel<"):
         return False
     args = [x.strip() for x in name[name.index("<") + 1:name.rindex(">")].split(",")]
@@ -290,6 +293,18 @@ def summarize(kt_dir: str, fetch_dir: str, write_dir: str, calib_mb: float, work
     return text
 
 
+def copy_calibration(torch, mb: float):
+    """A plain copy kernel of known size (mb MB read, mb MB written) for
+    scaling the FETCH_SIZE / WRITE_SIZE counters."""
+    n = int(mb * 1e6) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def ragged_workload_name(a) -> str:
     bx, by = a.block.split("x")
     return (f"paged decode attention, ragged batch of {a.ragged} (T uniform in [{a.min_tokens},{a.tokens}]), "
@@ -331,6 +346,9 @@ def main_ragged(a, torch, gpu):
     def step(i):
         gpu.paged_decode_attention(qt, cache, params=params, partial=partial, stats=stats, out=out)
 
+    if a.copy_calibration_mb > 0:
+        copy_calibration(torch, a.copy_calibration_mb)
+    traffic = read_traffic(a.traffic, ragged_workload_name(a))
     log(f"timing {a.steps} steps (tile {params.tile_tokens}, {s} splits max)")
     ms_step, mode = time_graph(torch, step, a.steps, a.warmup, not a.no_graph)
 
@@ -382,7 +400,8 @@ def main_ragged(a, torch, gpu):
                    "k_format": a.k_format, "tail": a.tail, "tile_tokens": params.tile_tokens,
                    "splits_max": s, "timing": mode, "bytes_per_step": {**counts, "step": step_bytes_}},
         "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic["bytes"] if traffic else None,
+                     "traffic_source": traffic["source"] if traffic else None,
                      "kernel": "paged_attn_kernel (split + in-kernel merge)", "bytes_per_launch": step_bytes_,
                      "us_per_launch": round(ms_step * 1e3, 3)},
         "cpu_baseline": None,
@@ -400,7 +419,8 @@ def main_ragged(a, torch, gpu):
 def main(argv=None):
     a = parse_args(argv)
     if a.summarize:
-        print(summarize(*a.summarize, a.copy_calibration_mb, workload_name(a)))
+        print(summarize(*a.summarize, a.copy_calibration_mb,
+                        ragged_workload_name(a) if a.ragged else workload_name(a)))
         return 0
     if a.counters:
         print(summarize_counters(a.counters))
@@ -438,13 +458,7 @@ def main(argv=None):
     out = torch.empty((a.batch, a.query_heads, a.dim), dtype=torch.float32, device="cuda")
 
     if a.copy_calibration_mb > 0:
-        n = int(a.copy_calibration_mb * 1e6) // 4
-        src = torch.ones(n, dtype=torch.float32, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            torch.neg(src, out=dst)
-        torch.cuda.synchronize()
-        del src, dst
+        copy_calibration(torch, a.copy_calibration_mb)
 
     # One launch per step: the split kernel with the merge done by the last
     # split workgroup of each (sequence, kv head).
