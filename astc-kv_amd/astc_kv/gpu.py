@@ -150,9 +150,12 @@ def default_tile(batch: int, kv_heads: int, tokens: int, chunk: int, block: int 
 
 def tile_for_splits(tokens: int, splits: int, block_y: int, dim: int) -> int:
     """Tile giving exactly `splits` splits when possible (e.g. T2048 in 8
-    splits); tiles are multiples of 16 tokens (block_y is not a constraint)."""
+    splits): ceil(tokens / splits), rounded up to 16 tokens when that keeps the
+    split count (16-token splits are the kernel's natural grain; any tile is
+    accepted)."""
     tile = -(-tokens // splits)
-    return -(-tile // 16) * 16
+    t16 = -(-tile // 16) * 16
+    return t16 if -(-tokens // t16) == splits else tile
 
 
 @dataclass
@@ -438,10 +441,12 @@ def paged_params(cache: DevicePagedKV, query_heads: int, tile: int | None = None
         want = -(-sum(cache.lens) * cache.kv_heads // (12 * groups))
         tile = max(step, -(-want // step) * step)
         limit = (62 * P) // step * step
-        while (tile + P) * P >= 1 << 24:
+        while (tile + P) * P >= 1 << 24 and tile > step:
             limit -= step
             tile = min(tile, limit)
         tile = min(tile, limit, -(-max_t // step) * step)
+        if tile < step or (tile + P) * P >= 1 << 24:
+            raise ValueError(f"no legal split tile for page_tokens {P} (at most 4080 for 16-token steps)")
     cols = cache.v_blocks.shape[3]
     return AkvPagedParams(cache.batch, max_t, query_heads, cache.kv_heads, cache.dim, P, cache.block_table.shape[1],
                           cache.k_pages.shape[0], tile, -(-max_t // tile), LAYOUTS[cache.layout], cache.block_x,

@@ -395,21 +395,31 @@ struct WaveStats {
 // workgroup counts itself in `arrival` (one counter per (sequence, kv head));
 // the last of the S workgroups merges the G query heads' S states into `out`
 // exactly as merge_kernel does, and leaves the counter at zero for the next
-// launch. No workgroup waits for another. The states are written and read
-// with agent-scope atomic accesses (write-through stores, coherent loads), so
-// publishing them needs no L2 write-back or invalidation: the stores of every
-// wave complete (s_waitcnt 0) before the barrier, and the counter increment
-// comes after it.
+// launch. No workgroup waits for another.
+// Ordering is the memory model's release/acquire pair, not a hardware
+// argument: every wave's state stores happen before the workgroup barrier;
+// the first lane then issues an agent-scope release fence and the counter
+// increment, and the workgroup whose increment completes the count issues an
+// agent-scope acquire fence before its barrier, so the states of all S
+// workgroups (on any XCD) happen before its loads. The states themselves are
+// written and read with agent-scope atomic accesses.
 // S: splits of this (sequence, kv head); SS: the split stride of partial and
 // stats (S for a uniform batch).
 template <int D, int G>
 __device__ inline void merge_if_last(uint32_t* arrival, const float* partial, const float2* stats,
                                      float* __restrict__ out, size_t qh0, int S, int SS, WaveStats& ws, float* lds,
                                      int lds_floats) {
+    // Each wave's state stores complete before the barrier (the workgroup
+    // barrier alone does not wait for global stores to be acknowledged).
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0)
-        ws.last = __hip_atomic_fetch_add(arrival, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == uint32_t(S - 1);
+    if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        const bool last =
+            __hip_atomic_fetch_add(arrival, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == uint32_t(S - 1);
+        if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        ws.last = last;
+    }
     __syncthreads();
     if (!ws.last) return;
     const int tid = threadIdx.x;

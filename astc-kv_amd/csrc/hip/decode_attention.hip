@@ -67,9 +67,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
     const uint16_t* sseq = DUMP ? nullptr : vscale + seq_kv * p.tokens;
     const uint16_t* oseq = DUMP ? nullptr : voffset + seq_kv * p.tokens;
 
-    // Splits and chunks start on 16-token boundaries, not block rows: a chunk
-    // covers the block rows from row c0 / by, starting at row offset c0 % by
-    // (a block row split between two chunks is decoded by both).
+    // Splits and chunks start at any token, not on block rows: a chunk covers
+    // the block rows from row c0 / by, starting at row offset c0 % by (a block
+    // row split between two chunks is decoded by both).
     auto chunk_blocks = [&](int c0) { return int((c0 % by + min(CT, split_end - c0) + by - 1) / by * cols); };
     auto k_rsrc = [&](int c0) {
         return seq_rsrc(DUMP ? nullptr : kseq + size_t(c0) * D, DUMP ? 0u : uint32_t(min(CT, split_end - c0)) * D * 2);
@@ -473,7 +473,6 @@ int check_astc(const AkvAttnParams* p) {
     if (bx < 4 || by < 4 || bx > 12 || by > 12 || bx * by > uint32_t(akv::kMaxTexels)) return AKV_HIP_ERR_FOOTPRINT;
     const uint32_t texcols = p->layout == AKV_LAYOUT_SCALAR ? p->dim : p->dim / 4;
     if (p->atlas_cols != (texcols + bx - 1) / bx) return AKV_HIP_ERR_SHAPE;
-    if (p->tile_tokens % 16) return AKV_HIP_ERR_TILE;
     if (uint64_t(p->atlas_rows) * by < p->tokens) return AKV_HIP_ERR_SHAPE;
     return 0;
 }
@@ -486,18 +485,23 @@ int plan_chunks(const AkvAttnParams* p, bool astc, KernelArgs* a) {
     using C = Cfg<D, NCH, WIDE>;
     uint32_t tokens = C::kMaxTok;
     if (astc) {
-        // Chunks start on 16-token boundaries, at row offset c0 % by <= by -
-        // gcd(16, by) of their first block row: the most tokens whose block
-        // rows fit the header stage at the worst offset, then whole rounds of
-        // tile groups (every wave the same number of tiles) where that fits,
-        // else whole tiles.
+        // A chunk starts at c0 = split * tile + k * chunk, where the chunk is
+        // the whole split or a multiple of 16 tokens, so every start is a
+        // multiple of g = gcd(16, tile, by) and sits at row offset c0 % by <=
+        // by - g of its first block row: the most tokens whose block rows fit
+        // the header stage at the worst offset, then whole rounds of tile
+        // groups (every wave the same number of tiles) where that fits, else
+        // whole tiles.
         const uint32_t by = p->block_y;
-        uint32_t g16 = 16, r16 = by;
-        while (r16) {
-            const uint32_t t = g16 % r16;
-            g16 = r16;
-            r16 = t;
-        }
+        auto gcd = [](uint32_t x, uint32_t y) {
+            while (y) {
+                const uint32_t t = x % y;
+                x = y;
+                y = t;
+            }
+            return x;
+        };
+        const uint32_t g16 = gcd(gcd(16, p->tile_tokens), by);
         const uint32_t rows = uint32_t(C::kMaxBlocks) / p->atlas_cols;
         if (rows * by <= by - g16) return AKV_HIP_ERR_SHAPE;
         tokens = std::min(rows * by - (by - g16), uint32_t(C::kMaxTok));
@@ -740,8 +744,9 @@ const char* akv_hip_error_string(int code) {
         case AKV_HIP_ERR_NULL: return "required pointer is NULL";
         case AKV_HIP_ERR_SHAPE: return "unsupported or inconsistent shape";
         case AKV_HIP_ERR_FOOTPRINT: return "unsupported ASTC footprint";
-        case AKV_HIP_ERR_TILE: return "tile_tokens/splits inconsistent (tile must be a positive multiple of 16 "
-                                      "and splits = ceil(tokens/tile))";
+        case AKV_HIP_ERR_TILE: return "tile_tokens/splits inconsistent (tile must be positive and "
+                                      "splits = ceil(tokens/tile); paged: tile a multiple of 16 and of "
+                                      "block_y, at most 62 pages)";
         case AKV_HIP_ERR_ALIGN: return "q, k, v and the V blocks must be 16-byte aligned";
         default: return code > 0 ? hipGetErrorString(hipError_t(code)) : "unknown error";
     }

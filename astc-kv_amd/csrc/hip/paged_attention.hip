@@ -86,8 +86,18 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
     // and in a ragged batch the XCDs holding the late splits of only the
     // long sequences idle while the others work: up to 2x slower.)
     const int kh = blockIdx.x, b = blockIdx.y, split = blockIdx.z;
-    const int len = lens[b];
+    // Lengths come from device memory: a length past max_tokens is read as
+    // max_tokens (the launched splits cover exactly that many, and the merge
+    // counts the splits of the clamped length); a sequence of no tokens gets
+    // zeros from its first split and no merge.
+    const int len = min(lens[b], int(p.max_tokens));
     const int P = int(p.page_tokens);
+    const size_t qh0 = size_t(b) * p.query_heads + size_t(kh) * G;
+    if (len <= 0) {
+        if (split == 0)
+            for (int i = tid; i < G * D; i += kThreads) out[qh0 * D + i] = 0.0f;
+        return;
+    }
     const int split_begin = split * int(p.tile_tokens);
     if (split_begin >= len) return;   // this sequence has fewer splits (uniform, before any barrier)
     const int split_end = min(split_begin + int(p.tile_tokens), len);
@@ -98,6 +108,10 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
     const int cols = int(p.atlas_cols), rpp = int(a.rows_per_page), Hkv = int(p.kv_heads);
     const int32_t* seq_table = table + size_t(b) * p.max_pages + page0;
     const uint16_t* tail = vtail ? vtail + (size_t(b) * Hkv + kh) * P * D : nullptr;
+    // Page ids come from device memory too: an id outside [0, num_pages) is
+    // read as page 0 (nothing outside the pools is touched) and poisons the
+    // sequence, whose output becomes NaN.
+    auto page_id = [&](int32_t id) { return uint32_t(id) < p.num_pages ? int(id) : 0; };
 
     // Page of a token: (page id, token within the page); t_abs - base_tok < tile + page.
     auto page_of = [&](int t_abs, int& pid, int& pos) {
@@ -117,7 +131,7 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
         // for; c0 and base_tok are uniform, so this is one scalar division.
         const int grow = (c0 - base_tok) / by + r;
         const int pg = int(fdiv(uint32_t(grow), a.mag_rpp)), prow = grow - pg * rpp;
-        const int pid = from_table ? seq_table[pg] : shp.pages[pg];
+        const int pid = from_table ? page_id(seq_table[pg]) : shp.pages[pg];
         return vpool[((size_t(pid) * Hkv + kh) * rpp + prow) * cols + col];
     };
 
@@ -128,7 +142,12 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
     QStage<D, G> qst;
     if (wave == 0) qst.load(q + (size_t(b) * p.query_heads + size_t(kh) * G) * D);
     uint4 raw = load_blk(split_begin, chunk_blocks(split_begin), true);
-    if (tid < npages) shp.pages[tid] = seq_table[tid];
+    int bad_page = 0;
+    if (tid < npages) {
+        const int32_t id = seq_table[tid];
+        bad_page = uint32_t(id) >= p.num_pages;
+        shp.pages[tid] = page_id(id);
+    }
     tables.store(sh.tabs, tid);
     if (wave == 0) qst.store(a.qscale, &sh.q[0][0]);
     if (tid < kPathKeys) sh.key_count[tid] = 0;
@@ -174,7 +193,7 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
         }
     };
 
-    __syncthreads();   // pages, decode tables and Q operands
+    const bool poisoned = __syncthreads_or(bad_page);   // pages, decode tables and Q operands
     for (int c0 = split_begin; c0 < split_end; c0 += CT) {
         const int ntok = min(CT, split_end - c0);
         const int ntiles = (ntok + 15) >> 4;
@@ -278,8 +297,8 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
         }
         __syncthreads();   // descriptors and so are rewritten by the next chunk
     }
-    const size_t qh0 = size_t(b) * p.query_heads + size_t(kh) * G;
     const int S = int(p.splits), Sb = (len + int(p.tile_tokens) - 1) / int(p.tile_tokens);
+    if (poisoned) st.l = __builtin_nanf("");   // a NaN sum of weights reaches every merge of this sequence
     combine_waves<D, NCH, G>(sh.u.comb, sh.ws, st, partial, stats, qh0, S, split);
     merge_if_last<D, G>(arrivals + size_t(b) * Hkv + kh, partial, stats, out, qh0, Sb, S, sh.ws, sh.u.comb,
                         kWaves * D * kMaxG);
@@ -398,7 +417,12 @@ int check_pool(const AkvPagedParams* p) {
     const uint32_t texcols = p->layout == AKV_LAYOUT_SCALAR ? p->dim : p->dim / 4;
     if (p->atlas_cols != (texcols + bx - 1) / bx) return AKV_HIP_ERR_SHAPE;
     const uint32_t P = p->page_tokens;
-    if (P == 0 || P % 16 || P % by || P > 4096) return AKV_HIP_ERR_SHAPE;
+    if (P == 0 || P % 16 || P % by) return AKV_HIP_ERR_SHAPE;
+    // The smallest legal tile, lcm(16, block_y) tokens, must pass check_paged's
+    // 24-bit bound on split-relative offsets (P <= 4080 for block_y = 4 or 8).
+    uint32_t step = 16;
+    while (step % by) step += 16;
+    if (uint64_t(step + P) * P >= (1u << 24)) return AKV_HIP_ERR_SHAPE;
     return 0;
 }
 

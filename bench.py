@@ -488,7 +488,9 @@ def main(argv=None):
 
     def fstep(i):
         kk, vv = fpool[i % len(fpool)]
-        gpu.fp16_attention(qt, kk, vv, params=fparams, partial=fpart, stats=fstat, out=out)
+        # Split + merge launches: the control's fastest form (its one-launch
+        # merge pays an L2 write-back per workgroup for the release fence).
+        gpu.fp16_attention(qt, kk, vv, params=fparams, partial=fpart, stats=fstat, out=out, fused=False)
 
     ms_fp16, _ = time_graph(torch, fstep, a.steps, a.warmup, not a.no_graph)
     fp16_bytes = nbytes["k"] * 2 + nbytes["q"] + nbytes["out"]

@@ -74,8 +74,9 @@ typedef struct AkvAttnParams {
     uint32_t kv_heads;
     uint32_t dim;           /* 64 or 128 */
     uint32_t page_tokens;   /* atlas padding unit (informational) */
-    uint32_t tile_tokens;   /* tokens per split: a positive multiple of 16 (splits need not
-                               start on a block row; a shared row is decoded by both) */
+    uint32_t tile_tokens;   /* tokens per split, any positive count as in the reference
+                               (probe_gqa_v10.mm:466; splits need not start on a block row,
+                               a shared row is decoded by both) */
     uint32_t splits;        /* ceil(tokens / tile_tokens) */
     uint32_t layout;        /* AKV_LAYOUT_SCALAR or AKV_LAYOUT_RGBA */
     uint32_t block_x;

@@ -81,6 +81,15 @@ def test_chunk_tokens_follow_the_footprint(hip):
     # D128 RGBA 4x4: 8 block columns, at most 256 blocks -> 32 rows = 128 tokens.
     p = c3(dim=128, block_x=4, block_y=4, atlas_cols=8, atlas_rows=2048, tile_tokens=8192, splits=1)
     assert hip.akv_hip_task_tokens(ct.byref(p), 1) == 128
+    # Any tile is legal (probe_gqa_v10.mm:466). Chunks then start at any token,
+    # at most by - gcd(16, tile, by) tokens into their first block row.
+    assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=238, splits=35)), 1) == 238
+    assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=1, splits=8192)), 1) == 1
+    s66 = dict(layout=0, block_x=6, block_y=6, atlas_cols=11, atlas_rows=1366)
+    # scalar 6x6: tile 200 -> starts are even, at most 4 in -> 84 - 4 = 80;
+    # tile 201 -> at most 5 in -> 79 -> whole tiles: 64.
+    assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=200, splits=41, **s66)), 1) == 80
+    assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=201, splits=41, **s66)), 1) == 64
     # FP16 control: whole 320-token chunks (128 for D128).
     assert hip.akv_hip_task_tokens(ct.byref(c3(tile_tokens=8192, splits=1)), 0) == 320
     assert hip.akv_hip_task_tokens(ct.byref(c3(dim=128, tile_tokens=8192, splits=1)), 0) == 128
@@ -96,7 +105,6 @@ def test_chunk_tokens_follow_the_footprint(hip):
     (dict(layout=7), -2),
     (dict(block_x=3), -3),                            # footprint below 4
     (dict(block_x=10, block_y=8, atlas_cols=2), -3),  # more than 64 texels
-    (dict(tile_tokens=238, splits=35), -4),           # tile not a multiple of 16
     (dict(splits=34), -4),                            # splits != ceil(T / tile)
     (dict(tile_tokens=0), -4),
 ])
