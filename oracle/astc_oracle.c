@@ -24,13 +24,26 @@
  *
  * Pinned against astcenc's archived outputs (the reference's fixtures): 6x6
  * blocks with endpoint modes 0/1, 1-4 partitions, reduced weight grids,
- * trit/quint weights of 4-20 levels, and the UNORM16 -> FP16 rule. Pinned by
- * closed forms: trit/quint block codes, integer-sequence bit counts,
- * unquantisation levels, void extent, small-block partition coordinates.
- * PARITY UNPINNED (no astcenc vector exists for them here; checked only by
- * agreement with the separately written product decoders and by encoder
- * round trips): endpoint modes 4-13 (RGB/RGBA, blue contraction, bit
- * transfer), dual-plane blocks, footprints other than 6x6, and HDR modes.
+ * trit/quint weights, colour ranges of 10 to 256 levels (all but 16), and the
+ * UNORM16 -> FP16 rule. Pinned by reduction to those blocks (tests/test_oracle_reductions.py,
+ * with a specification-written block writer that is itself checked against
+ * every archived block): endpoint modes 1 and 4-13 (direct, swapped with blue
+ * contraction, bit transfer, base+scale, alpha pairs, partitions mixing
+ * endpoint classes), dual-plane blocks, identity weight grids and reduced
+ * grids of every footprint up to 64 texels. Pinned by closed forms: trit/quint
+ * block codes, integer-sequence bit counts, unquantisation levels, void
+ * extent, small-block partition coordinates. Each of eleven planted mistakes
+ * (missing blue contraction, 5-bit offsets, swapped planes, swapped alpha
+ * pairs, ...) fails at least one of these tests.
+ * PARITY UNPINNED (no astcenc vector, no reduction reaches them): HDR modes
+ * (decode to the error colour); the partition hash at coordinates above 5
+ * (footprints under 31 texels, such as 6x5, evaluate it at doubled
+ * coordinates up to (10, 8); the same arithmetic as the pinned 0..5); which
+ * colour channel each endpoint value feeds (the specification's table;
+ * luminance data cannot tell channels apart); colour unquantisation of the
+ * 6-, 8- and 16-level ranges and weight unquantisation of the 12-, 20-, 24-
+ * and 32-level ranges, which astcenc never chose on the archived data (closed
+ * forms only).
  */
 #include <stdint.h>
 #include <string.h>

@@ -12,7 +12,10 @@ NumPy restatements of the reference's numerics on the decode-attention path:
                           their exact merge), in float64
 * `fp16_floor/fp16_ceil` astc_kv/codec.py:70-81
 * `normalize_token`      astc_kv/codec.py:162-166, :175-180
-* `affine_quantize`      astc_kv/codec.py:218-250
+* `affine_quantize`      astc_kv/codec.py:218-250 (pinned by outputs of the reference
+                          module itself, tests/golden/gen_affine_quantize.py)
+* `normalize_token` is pinned by the reference's captured normalisation
+  (scripts/probe_block_geometry.py:142-155 -> tests/golden/geometry/*_fixed_input.npz)
 """
 from __future__ import annotations
 

@@ -5,9 +5,11 @@ Run in a container where the reference checkout is mounted (default
 /root/reference). Only data files are copied: astcenc 5.7.0 payloads
 (.astc/.bin), the reference's astcenc-decoded and restored tensors
 (*_decoded.f32, *.npy), fp16 metadata and queries. For the block-geometry
-captures only the fp16 offsets/scales are extracted from fixed_input.npz
-(numpy.load with allow_pickle=False). Writes PROVENANCE.json with the SHA256
-of every source file.
+captures the arrays of fixed_input.npz are extracted (numpy.load with
+allow_pickle=False): the captured V prefix, its fp16 token offsets/scales and
+the normalised, edge-padded scalar image the reference encoded
+(scripts/probe_block_geometry.py:142-155). Writes PROVENANCE.json with the
+SHA256 of every source file.
 
 Sources (relative to the reference root):
   results/kernel_v2/fixtures_page/{t384,t391}         scalar 6x6, token-normalised V
@@ -69,6 +71,11 @@ def main():
             prov[str(dst.relative_to(HERE))] = {"source": str((src / "fixed_input.npz").relative_to(args.reference)),
                                                 "sha256": sha(src / "fixed_input.npz"),
                                                 "extracted": ["fp16_offsets", "fp16_scales"]}
+            dst = HERE / "geometry" / f"{cap}_fixed_input.npz"
+            keys = ["original_v_prefix", "normalized_padded", "fp16_offsets", "fp16_scales"]
+            np.savez_compressed(dst, **{k: z[k] for k in keys})
+            prov[str(dst.relative_to(HERE))] = {"source": str((src / "fixed_input.npz").relative_to(args.reference)),
+                                                "sha256": sha(src / "fixed_input.npz"), "extracted": keys}
     for f in HOLDOUT:
         copy(res / "geometry_holdout_v2" / f"{f}.bin", HERE / "holdout" / (f.replace("/", "_") + ".bin"))
     (HERE / "PROVENANCE.json").write_text(json.dumps(prov, indent=1, sort_keys=True) + "\n")

@@ -133,6 +133,44 @@ def test_quantizer_codes_match_oracle_and_invariants(bits, axis, group):
     np.testing.assert_array_equal(unpacked[: flat.size], flat)
 
 
+def test_affine_quantize_matches_reference_vectors(golden):
+    """The product quantiser against outputs of the reference's own
+    affine_quantize (tests/golden/gen_affine_quantize.py), ties included."""
+    import json
+    meta = json.loads((golden / "affine_quantize.json").read_text())
+    with np.load(golden / "affine_quantize.npz", allow_pickle=False) as z:
+        for c in meta["cases"]:
+            dec, counts = codec.affine_quantize(z[c["input"] + "__x"], c["bits"], c["axis"], c["group"])
+            assert np.array_equal(dec.view(np.uint32), z[c["key"]].view(np.uint32)), c["key"]
+            assert counts == c["counts"]
+
+
+@pytest.mark.parametrize("cap", ["records_l17", "science_l5"])
+def test_normalisation_and_packing_match_reference_capture(golden, cap):
+    """codec.encode_tensor's token normalisation and scalar packing
+    (codec.py:162-166, :181-187) and atlas.normalize_tokens on a captured V
+    prefix reproduce the reference's fp16 offsets/scales and padded image."""
+    from astc_kv.atlas import normalize_tokens
+    with np.load(golden / "geometry" / f"{cap}_fixed_input.npz", allow_pickle=False) as z:
+        x, padded, off, sc = z["original_v_prefix"], z["normalized_padded"], z["fp16_offsets"], z["fp16_scales"]
+    heads, tokens, dim = x.shape
+    u, o, s = codec._range_normalize(x, "token", heads, tokens, dim, 66, 6, 6, 96)
+    assert np.array_equal(o.view(np.uint16), off.view(np.uint16))
+    assert np.array_equal(s.view(np.uint16), sc.view(np.uint16))
+    image = codec.pack_images(np.clip(u, 0, 1), "scalar", 66)
+    assert np.array_equal(image[..., 0].view(np.uint32), padded.view(np.uint32))
+    assert np.all(image[..., 0] == image[..., 1]) and np.all(image[..., 3] == 1)
+    u2, o2, s2 = normalize_tokens(x)
+    assert np.array_equal(o2.view(np.uint16), off[..., 0].view(np.uint16))
+    assert np.array_equal(s2.view(np.uint16), sc[..., 0].view(np.uint16))
+    assert np.array_equal(u2.view(np.uint32), padded[..., :dim].view(np.uint32))
+    # The byte accounting of the same encode (reference row: 25344 + 1728 + 1728).
+    with patch("astc_kv.codec.AstcEncoder", IdentityAstc):
+        t = codec.encode_tensor(x, dict(layout="scalar", block=6, normalization="token"))
+    assert t.byte_counts == {"astc_blocks_including_edge_padding": 25344, "fp16_offsets": 1728,
+                             "fp16_scales": 1728, "permutation_map": 0}
+
+
 # --- the product CPU codec against the oracle ------------------------------------
 
 def product_decode(blocks, bx, by):

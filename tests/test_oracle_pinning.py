@@ -180,3 +180,30 @@ def test_block_mode_header_examples():
     blk = bytes([0xFC, 0x01]) + bytes(14)
     _, kind = O.decode_block_unorm16(blk, 6, 6)
     assert kind in (1, 2)
+
+
+@pytest.mark.parametrize("cap", ["records_l17", "science_l5"])
+def test_token_normalisation_matches_reference_capture(golden, cap):
+    """The reference's own normalisation of two captured V prefixes
+    (scripts/probe_block_geometry.py:142-146, the code of codec.py:162-166):
+    fp16 offsets and scales and the clipped, edge-padded scalar image, bit for
+    bit, from the captured float32 values."""
+    with np.load(golden / "geometry" / f"{cap}_fixed_input.npz", allow_pickle=False) as z:
+        x, padded, off, sc = z["original_v_prefix"], z["normalized_padded"], z["fp16_offsets"], z["fp16_scales"]
+    u, o, s = R.normalize_token(x)
+    assert np.array_equal(o.view(np.uint16), off.view(np.uint16))
+    assert np.array_equal(s.view(np.uint16), sc.view(np.uint16))
+    mine = np.pad(u, ((0, 0), (0, 0), (0, padded.shape[-1] - u.shape[-1])), mode="edge")
+    assert np.array_equal(mine.view(np.uint32), padded.view(np.uint32))
+
+
+def test_affine_quantize_matches_reference_vectors(golden):
+    """affine_quantize outputs written by the reference module itself
+    (tests/golden/gen_affine_quantize.py): 5 configurations x 3 inputs,
+    including exact half-step ties (round half to even)."""
+    meta = json.loads((golden / "affine_quantize.json").read_text())
+    with np.load(golden / "affine_quantize.npz", allow_pickle=False) as z:
+        for c in meta["cases"]:
+            dec, counts, *_ = R.affine_quantize(z[c["input"] + "__x"], c["bits"], c["axis"], c["group"])
+            assert np.array_equal(dec.view(np.uint32), z[c["key"]].view(np.uint32)), c["key"]
+            assert counts == c["counts"]
