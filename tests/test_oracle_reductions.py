@@ -262,11 +262,9 @@ def reachable(kind, r):
     return [(A, B) for A in range(256) for B in range(256) if A != B and _values(kind, A, B, r) is not None]
 
 
-@pytest.mark.parametrize("name", list(KINDS) + list(MIXED))
-def test_endpoint_modes_reduce_to_luminance(name):
-    """Archived blocks re-expressed with their own endpoints where the mode can
-    hold them, and with drawn endpoints on the same mode, weights and
-    partitions otherwise (at least 200 blocks per mode)."""
+@lru_cache(maxsize=None)
+def endpoint_mode_blocks(name):
+    """(source blocks, the same blocks re-expressed in endpoint mode(s) `name`)."""
     kinds = MIXED.get(name, (name,))
     rng = np.random.default_rng(sum(map(ord, name)))
     src, built, exact = [], [], 0
@@ -274,11 +272,21 @@ def test_endpoint_modes_reduce_to_luminance(name):
         got = _reexpress(f, kinds)
         if got is not None:
             exact += 1
-        elif len(built) < 300 + exact:
+        elif len(built) < 250 + exact:
             got = _reexpress(f, kinds, rng)
         if got is not None:
             src.append(got[0] or b)
             built.append(got[1])
+    return src, built
+
+
+@pytest.mark.parametrize("name", list(KINDS) + list(MIXED))
+def test_endpoint_modes_reduce_to_luminance(name):
+    """Archived blocks re-expressed with their own endpoints where the mode can
+    hold them, and with drawn endpoints on the same mode, weights and
+    partitions otherwise (at least 200 blocks per mode)."""
+    kinds = MIXED.get(name, (name,))
+    src, built = endpoint_mode_blocks(name)
     assert len(built) >= 200, f"{name}: only {len(built)} blocks"
     # The re-expressed blocks really use the intended modes.
     for w in built[:50]:
@@ -355,16 +363,10 @@ def test_rgba_channels_are_separable():
     assert done >= 100
 
 
-@pytest.mark.parametrize("cem", [1, 4, 5, 6, 8, 9, 10, 12, 13])
-def test_endpoint_modes_channel_by_channel(cem):
-    """Random colour values in every LDR endpoint mode on the archived blocks'
-    modes and weights: each channel decodes like the luminance (mode 0) block
-    of that channel's endpoint pair, e0 -> e1 as the specification derives it
-    (tests/astc_spec.spec_endpoints: swap on the sums with blue contraction,
-    bit transfer, scale, alpha pairs). This is where channel routing, the
-    swap condition at equal sums (values chosen so that ties occur), blue
-    contraction and the alpha values are checked; the grey reductions above
-    cannot see them."""
+@lru_cache(maxsize=None)
+def channel_blocks(cem):
+    """(blocks of endpoint mode `cem` with random values, 4 luminance blocks
+    per block holding its channels' endpoint pairs, count of swap-boundary ties)."""
     rng = np.random.default_rng(100 + cem)
     nv = 2 * ((cem >> 2) + 1)
     built, lum, ties = [], [], 0
@@ -393,6 +395,20 @@ def test_endpoint_modes_channel_by_channel(cem):
         g.colours = q
         built.append(S.write_block(g))
         lum += refs
+    return built, lum, ties
+
+
+@pytest.mark.parametrize("cem", [1, 4, 5, 6, 8, 9, 10, 12, 13])
+def test_endpoint_modes_channel_by_channel(cem):
+    """Random colour values in every LDR endpoint mode on the archived blocks'
+    modes and weights: each channel decodes like the luminance (mode 0) block
+    of that channel's endpoint pair, e0 -> e1 as the specification derives it
+    (tests/astc_spec.spec_endpoints: swap on the sums with blue contraction,
+    bit transfer, scale, alpha pairs). This is where channel routing, the
+    swap condition at equal sums (values chosen so that ties occur), blue
+    contraction and the alpha values are checked; the grey reductions above
+    cannot see them."""
+    built, lum, ties = channel_blocks(cem)
     assert len(built) >= 250
     if cem in (8, 9, 12, 13):
         assert ties >= 5, ties
@@ -426,7 +442,9 @@ def _dual_cases():
                 yield S.write_block(f), f
 
 
-def test_dual_plane_equal_planes_is_single_plane():
+@lru_cache(maxsize=None)
+def dual_blocks():
+    """(single-plane blocks, the same as dual-plane blocks with equal planes)."""
     src, built = [], []
     for b, f in _dual_cases():
         ends = (unq_colour(f.crange)[f.colours[0]], unq_colour(f.crange)[f.colours[1]])
@@ -438,6 +456,11 @@ def test_dual_plane_equal_planes_is_single_plane():
             g.colours = [q_of(r, ends[0]), q_of(r, ends[1])]
             built.append(S.write_block(g))
             src.append(b)
+    return src, built
+
+
+def test_dual_plane_equal_planes_is_single_plane():
+    src, built = dual_blocks()
     a, _ = decode(src)
     c, kc = decode(built)
     assert len(built) >= 100 and np.all(kc == 0)
@@ -553,3 +576,28 @@ def test_reduced_grids_corners_constant_and_monotone(bx, by):
         assert np.all(tw[1] == unq[const[0]])
         assert np.all(np.diff(tw[2], axis=1) >= 0) and np.all(tw[2][:, 0] == 0) and np.all(tw[2][:, -1] == 64)
         assert np.all(tw[2] == tw[2][:1])      # a ramp along x is constant along y
+
+
+def constructed_blocks(bx, by):
+    """Every block these tests build for footprint bx x by, as uint8 [n, 16]
+    (6x6: endpoint-mode reductions, per-channel modes, dual plane; all
+    footprints: identity and reduced weight grids), for the GPU decoders."""
+    out = []
+    if (bx, by) == (6, 6):
+        for name in list(KINDS) + list(MIXED):
+            out += endpoint_mode_blocks(name)[1]
+        for cem in (1, 4, 5, 6, 8, 9, 10, 12, 13):
+            out += channel_blocks(cem)[0]
+        out += dual_blocks()[1]
+    wr = next(r for r in (0, 2, 5, 8) if 24 <= S.ise_bits(bx * by, r) <= 96)
+    for i in range(bx * by):
+        wts = [0] * (bx * by)
+        wts[i] = S.LEVELS[wr] - 1
+        out.append(_grid_block(bx, by, wr, wts))
+    rng = np.random.default_rng(bx * 31 + by)
+    for gw, gh, r in _modes_for(bx, by):
+        cr = S.colour_range(2, S.colour_bits_available(S.Block(gw, gh, r, [0] * gw * gh, [0], [0, 0])))
+        for _ in range(4):
+            A, B = sorted(int(x) for x in rng.choice(unq_colour(cr), 2))
+            out.append(_grid_block(gw, gh, r, rng.integers(0, S.LEVELS[r], gw * gh).tolist(), A, B))
+    return np.frombuffer(b"".join(out), np.uint8).reshape(-1, 16)
