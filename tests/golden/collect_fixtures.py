@@ -29,7 +29,7 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 
-PAGE_FILES = ["manifest.json", "q.f32", "k.f16", "v-h000.astc", "v-h001.astc", "v-h002.astc",
+PAGE_FILES = ["manifest.json", "q.f32", "k.f16", "k_decoded.f32", "v-h000.astc", "v-h001.astc", "v-h002.astc",
               "v_decoded.f32", "v_scale.f16", "v_offset.f16"]
 KV_FILES = ["manifest.json", "q.f32"] + [f"{n}-h00{h}.astc" for n in "kv" for h in range(3)] + \
            [f"{n}_{s}" for n in "kv" for s in ("decoded.f32", "scale.f16", "offset.f16")]
