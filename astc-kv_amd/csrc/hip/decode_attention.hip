@@ -618,17 +618,19 @@ hipError_t launch_merge(const AkvAttnParams* p, const float* partial, const floa
     return hipGetLastError();
 }
 
+// `tab`: the footprint's decode tables on the current device, or NULL to use
+// (and on first use upload) the library's allocated copy.
 int run_astc(const AkvAttnParams* p, const float* q, const uint16_t* k, const void* v_blocks, const uint16_t* v_scale,
              const uint16_t* v_offset, float* partial, float* stats, float* out, bool with_merge, uint32_t* arrivals,
-             void* stream) {
+             void* stream, const AkvTables* tab = nullptr) {
     uint32_t G = 0;
     if (int rc = check_common(p, &G)) return rc;
     if (int rc = check_astc(p)) return rc;
     if (!q || !k || !v_blocks || !v_scale || !v_offset || !partial || !stats || (with_merge && !out))
         return AKV_HIP_ERR_NULL;
     if (!aligned16(q) || !aligned16(k) || !aligned16(v_blocks)) return AKV_HIP_ERR_ALIGN;
-    const AkvTables* tab = nullptr;
-    if (int rc = device_tables(int(p->block_x), int(p->block_y), &tab)) return rc;
+    if (!tab)
+        if (int rc = device_tables(int(p->block_x), int(p->block_y), &tab)) return rc;
     KernelArgs a;
     if (int rc = make_args(p, true, &a)) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -642,12 +644,111 @@ int run_astc(const AkvAttnParams* p, const float* q, const uint16_t* k, const vo
     return as_int(e);
 }
 
+// --- the entry point that allocates nothing ----------------------------------
+//
+// akv_hip_decode_attention_noalloc keeps the one-launch step's workspace in a
+// static device array instead of caller memory: the split states (partial,
+// stats), the arrival counters and the decode tables of up to four footprints.
+// Each GPU holds its own copy for the life of the process. Layout:
+//   [0, 256 KiB)           four 64 KiB decode-table slots, one per footprint
+//   [256 KiB, 512 KiB)     65,536 arrival counters (uint32), zero between calls
+//   [512 KiB, 8.5 MiB)     split states: partial f32 [B][Hq][S][D], then stats
+constexpr size_t kNaSlots = 4, kNaSlotBytes = 65536;
+constexpr size_t kNaCounters = 65536;
+constexpr size_t kNaStateBytes = size_t(8) << 20;
+constexpr size_t kNaCounterOff = kNaSlots * kNaSlotBytes;
+constexpr size_t kNaStateOff = kNaCounterOff + kNaCounters * sizeof(uint32_t);
+constexpr size_t kNaBytes = kNaStateOff + kNaStateBytes;
+static_assert(sizeof(AkvTables) <= kNaSlotBytes, "a table slot holds one footprint's tables");
+
+static __device__ __align__(256) unsigned char scratch[kNaBytes];
+
+__global__ void zero_words_kernel(uint32_t* p, uint32_t n) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+struct NoAllocDevice {
+    unsigned char* base = nullptr;   // the device address of `scratch` on this GPU
+    int slot_bx[kNaSlots] = {}, slot_by[kNaSlots] = {};
+    int used = 0;
+};
+
+std::mutex g_na_mu;
+std::map<int, NoAllocDevice> g_na;   // per device
+
+// The current device's scratch address and the table slot of footprint (bx,
+// by). The first call on a device looks the address up (hipGetSymbolAddress)
+// and clears the arrival counters with a fill kernel on `st`; the first call
+// for a footprint copies its tables into a free slot (a blocking copy from
+// host memory, no allocation).
+int noalloc_setup(int bx, int by, hipStream_t st, unsigned char** base, const AkvTables** tab) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return int(e);
+    std::lock_guard<std::mutex> lock(g_na_mu);
+    NoAllocDevice& d = g_na[dev];
+    if (!d.base) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            g_na.erase(dev);
+            return e != hipSuccess ? int(e) : int(hipErrorInvalidSymbol);
+        }
+        unsigned char* b = static_cast<unsigned char*>(ptr);
+        zero_words_kernel<<<dim3(64), dim3(kThreads), 0, st>>>(reinterpret_cast<uint32_t*>(b + kNaCounterOff),
+                                                                uint32_t(kNaCounters));
+        e = hipGetLastError();
+        if (e != hipSuccess) {
+            g_na.erase(dev);
+            return int(e);
+        }
+        d.base = b;
+    }
+    int slot = -1;
+    for (int i = 0; i < d.used; ++i)
+        if (d.slot_bx[i] == bx && d.slot_by[i] == by) slot = i;
+    if (slot < 0) {
+        if (d.used == int(kNaSlots)) return AKV_HIP_ERR_SCRATCH;
+        const AkvTables* host = akv::tables_for(bx, by);
+        if (!host) return AKV_HIP_ERR_FOOTPRINT;
+        e = hipMemcpy(d.base + d.used * kNaSlotBytes, host, sizeof(AkvTables), hipMemcpyHostToDevice);
+        if (e != hipSuccess) return int(e);
+        slot = d.used++;
+        d.slot_bx[slot] = bx;
+        d.slot_by[slot] = by;
+    }
+    *base = d.base;
+    *tab = reinterpret_cast<const AkvTables*>(d.base + slot * kNaSlotBytes);
+    return 0;
+}
+
 }  // namespace
 }  // namespace akv_hip
 
 using namespace akv_hip;
 
 extern "C" {
+
+int akv_hip_decode_attention_noalloc(const AkvAttnParams* p, const float* q, const uint16_t* k, const void* v_blocks,
+                                     const uint16_t* v_scale, const uint16_t* v_offset, float* out, void* stream) {
+    uint32_t G = 0;
+    if (int rc = check_common(p, &G)) return rc;
+    if (int rc = check_astc(p)) return rc;
+    if (!q || !k || !v_blocks || !v_scale || !v_offset || !out) return AKV_HIP_ERR_NULL;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v_blocks)) return AKV_HIP_ERR_ALIGN;
+    const uint64_t states = uint64_t(p->batch) * p->query_heads * p->splits * p->dim;
+    if ((states + uint64_t(p->batch) * p->query_heads * p->splits * 2) * sizeof(float) > kNaStateBytes ||
+        uint64_t(p->batch) * p->kv_heads > kNaCounters)
+        return AKV_HIP_ERR_SCRATCH;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    unsigned char* base = nullptr;
+    const AkvTables* tab = nullptr;
+    if (int rc = noalloc_setup(int(p->block_x), int(p->block_y), st, &base, &tab)) return rc;
+    float* partial = reinterpret_cast<float*>(base + kNaStateOff);
+    float* stats = partial + states;   // states is a multiple of 64: 8-byte aligned
+    uint32_t* arrivals = reinterpret_cast<uint32_t*>(base + kNaCounterOff);
+    return run_astc(p, q, k, v_blocks, v_scale, v_offset, partial, stats, out, true, arrivals, stream, tab);
+}
 
 int akv_hip_attention_split(const AkvAttnParams* p, const float* q, const uint16_t* k, const void* v_blocks,
                             const uint16_t* v_scale, const uint16_t* v_offset, float* partial, float* stats,
@@ -748,6 +849,9 @@ const char* akv_hip_error_string(int code) {
                                       "splits = ceil(tokens/tile); paged: tile a multiple of 16 and of "
                                       "block_y, at most 62 pages)";
         case AKV_HIP_ERR_ALIGN: return "q, k, v and the V blocks must be 16-byte aligned";
+        case AKV_HIP_ERR_SCRATCH: return "request exceeds the static scratch of akv_hip_decode_attention_noalloc "
+                                         "(split states batch*query_heads*splits*(dim+2)*4 bytes <= 8 MiB, "
+                                         "batch*kv_heads <= 65536, at most 4 footprints per device)";
         default: return code > 0 ? hipGetErrorString(hipError_t(code)) : "unknown error";
     }
 }

@@ -59,7 +59,8 @@ enum {
     AKV_HIP_ERR_SHAPE = -2,       /* unsupported or inconsistent shape */
     AKV_HIP_ERR_FOOTPRINT = -3,   /* unsupported ASTC footprint */
     AKV_HIP_ERR_TILE = -4,        /* tile_tokens/splits inconsistent */
-    AKV_HIP_ERR_ALIGN = -5        /* q, k, v or the V blocks not 16-byte aligned */
+    AKV_HIP_ERR_ALIGN = -5,       /* q, k, v or the V blocks not 16-byte aligned */
+    AKV_HIP_ERR_SCRATCH = -6      /* beyond the static scratch of the no-allocation entry point */
 };
 
 enum { AKV_LAYOUT_SCALAR = 0, AKV_LAYOUT_RGBA = 1 };
@@ -99,6 +100,22 @@ int akv_hip_decode_attention(const AkvAttnParams* p, const float* q, const uint1
 int akv_hip_decode_attention_fused(const AkvAttnParams* p, const float* q, const uint16_t* k, const void* v_blocks,
                                    const uint16_t* v_scale, const uint16_t* v_offset, float* partial, float* stats,
                                    float* out, uint32_t* arrivals, void* stream);
+
+/* As akv_hip_decode_attention_fused, allocating nothing. No counterpart in
+   the reference; for callers that cannot allocate device memory (code under
+   HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+   The split states, arrival counters and decode tables live in a static
+   device array of the library, 8.5 MiB per GPU, held until the process ends:
+   limits batch * query_heads * splits * (dim + 2) * 4 bytes <= 8 MiB,
+   batch * kv_heads <= 65536 and at most 4 footprints per device (else
+   AKV_HIP_ERR_SCRATCH, nothing launched). The first call on a device clears
+   the counters with a fill kernel on `stream`; the first call per footprint
+   and device copies that footprint's decode tables (blocking): make those
+   first calls outside graph capture. Every call leaves the counters zero.
+   All calls on one GPU share the array: calls that overlap in time on one
+   GPU (concurrent streams, threads) race. */
+int akv_hip_decode_attention_noalloc(const AkvAttnParams* p, const float* q, const uint16_t* k, const void* v_blocks,
+                                     const uint16_t* v_scale, const uint16_t* v_offset, float* out, void* stream);
 
 int akv_hip_attention_split(const AkvAttnParams* p, const float* q, const uint16_t* k, const void* v_blocks,
                             const uint16_t* v_scale, const uint16_t* v_offset, float* partial, float* stats,
