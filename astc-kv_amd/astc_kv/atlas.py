@@ -82,6 +82,41 @@ class Atlas:
         return u * self.scale.astype(np.float32)[..., None] + self.offset.astype(np.float32)[..., None]
 
 
+def block_class_histogram(blocks: np.ndarray, block_x: int, block_y: int, layout: str) -> dict:
+    """How the GPU decoder will treat an atlas's blocks (what its decode cost
+    depends on): fractions of void-extent and error blocks, of blocks whose
+    texels come from the per-block table (identity weight grid, one plane,
+    partitions x weight levels <= 8 RGBA / 32 scalar entries) or are computed,
+    of reduced weight grids and dual-plane blocks, and histograms of partition
+    counts, weight levels and endpoint modes (libakv_astc akv_block_classes)."""
+    lib = codec.load_codec_library()
+    flat = np.ascontiguousarray(blocks, np.uint8).reshape(-1, 16)
+    n = flat.shape[0]
+    cls = np.empty(n, np.uint32)
+    rc = lib.akv_block_classes(block_x, block_y, flat.ctypes.data, n, cls.ctypes.data)
+    if rc:
+        raise RuntimeError(lib.akv_error(rc).decode())
+    kind = cls & 3
+    normal = kind == 0
+    parts = ((cls >> 2) & 3) + 1
+    dual = ((cls >> 4) & 1).astype(bool)
+    identity = ((cls >> 5) & 1).astype(bool)
+    levels = (cls >> 6) & 63
+    cem = (cls >> 12) & 15
+    entries = 32 if layout == "scalar" else 8
+    table = normal & identity & ~dual & (parts * levels <= entries)
+
+    def hist(values):
+        v, c = np.unique(values[normal], return_counts=True)
+        return {str(int(a)): round(float(b) / max(n, 1), 4) for a, b in zip(v, c)}
+
+    frac = lambda m: round(float(np.count_nonzero(m)) / max(n, 1), 4)  # noqa: E731
+    return {"blocks": int(n), "table_path": frac(table), "compute_path": frac(normal & ~table),
+            "reduced_grid": frac(normal & ~identity), "dual_plane": frac(normal & dual),
+            "void_extent": frac(kind == 1), "error": frac(kind == 2), "partitions": hist(parts),
+            "weight_levels": hist(levels), "endpoint_modes": hist(cem)}
+
+
 def texel_columns(dim: int, layout: str) -> int:
     return dim if layout == "scalar" else dim // 4
 

@@ -48,6 +48,7 @@ def load_codec_library(path: Path | None = None):
     lib.akv_decode.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_size_t, ct.c_void_p, ct.c_uint, ct.c_uint]
     lib.akv_encode_blocks.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_size_t, ct.c_void_p]
     lib.akv_decode_blocks_fp16.argtypes = [ct.c_uint, ct.c_uint, ct.c_void_p, ct.c_size_t, ct.c_void_p, ct.c_void_p]
+    lib.akv_block_classes.argtypes = [ct.c_uint, ct.c_uint, ct.c_void_p, ct.c_size_t, ct.c_void_p]
     return lib
 
 

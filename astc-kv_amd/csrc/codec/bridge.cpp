@@ -1,6 +1,7 @@
 // akv_* C-ABI of libakv_astc.so (declared in include/astc_kv.h).
 #include "astc_kv.h"
 
+#include <algorithm>
 #include <new>
 
 #include "astc_codec.h"
@@ -98,6 +99,65 @@ int akv_decode_blocks_fp16(unsigned bx, unsigned by, const uint8_t* blocks, size
     for (size_t i = 0; i < n; ++i) {
         int k = akv::decode_block_fp16(*t, blocks + 16 * i, texels + i * per);
         if (kinds) kinds[i] = k;
+    }
+    return AKV_SUCCESS;
+}
+
+int akv_block_classes(unsigned bx, unsigned by, const uint8_t* blocks, size_t n, uint32_t* out) {
+    const akv::AkvTables* t = akv::tables_for(int(bx), int(by));
+    if (!t) return AKV_ERR_BAD_BLOCK_SIZE;
+    if ((!blocks || !out) && n) return AKV_ERR_BAD_PARAM;
+    auto bits = [](const uint8_t* b, int start, int count) {   // little-endian bit field, count <= 24
+        uint32_t v = 0;
+        for (int k = 0; k < count; ++k) v |= uint32_t((b[(start + k) >> 3] >> ((start + k) & 7)) & 1) << k;
+        return v;
+    };
+    for (size_t i = 0; i < n; ++i) {
+        const uint8_t* b = blocks + 16 * i;
+        const uint32_t mode = bits(b, 0, 11);
+        if ((mode & 0x1FF) == 0x1FC) {
+            // Void extent: LDR only, and the extent either all ones or ordered.
+            const uint32_t s0 = bits(b, 12, 13), s1 = bits(b, 25, 13), t0 = bits(b, 38, 13), t1 = bits(b, 51, 13);
+            const bool all_ones = s0 == 0x1FFF && s1 == 0x1FFF && t0 == 0x1FFF && t1 == 0x1FFF;
+            out[i] = (bits(b, 9, 1) || (!all_ones && (s0 >= s1 || t0 >= t1))) ? AKV_CLASS_ERROR : AKV_CLASS_VOID;
+            continue;
+        }
+        const uint32_t md = t->block_mode[mode];
+        const uint32_t parts = bits(b, 11, 2) + 1;
+        if (!md || (akv::mode_dual(md) && parts == 4)) {
+            out[i] = AKV_CLASS_ERROR;
+            continue;
+        }
+        uint32_t cem[4] = {0, 0, 0, 0}, shared = 1;
+        int below = 128 - int(akv::mode_wbits(md)), config_start = 17;
+        if (parts == 1) {
+            cem[0] = bits(b, 13, 4);
+        } else {
+            config_start = 29;
+            const uint32_t field = bits(b, 23, 6);
+            if ((field & 3) == 0) {
+                for (uint32_t p = 0; p < parts; ++p) cem[p] = field >> 2;
+            } else {
+                shared = 0;
+                const int extra = 3 * int(parts) - 4;
+                below -= extra;
+                const uint32_t enc = field | bits(b, below, extra) << 6;
+                const uint32_t base = (enc & 3) - 1;
+                for (uint32_t p = 0; p < parts; ++p)
+                    cem[p] = (base + ((enc >> (2 + p)) & 1)) << 2 | ((enc >> (2 + parts + 2 * p)) & 3);
+            }
+        }
+        if (akv::mode_dual(md)) below -= 2;
+        int pairs = 0;
+        for (uint32_t p = 0; p < parts; ++p) pairs += int(cem[p] >> 2) + 1;
+        const int avail = below - config_start;
+        // Colour values must fit (at most 18) with at least 6 levels (range 4).
+        if (pairs > 9 || avail <= 0 || t->color_range[pairs][std::min(avail, 127)] < 4) {
+            out[i] = AKV_CLASS_ERROR;
+            continue;
+        }
+        out[i] = AKV_CLASS_NORMAL | (parts - 1) << 2 | akv::mode_dual(md) << 4 | akv::mode_identity(md) << 5 |
+                 uint32_t(t->weight_levels[akv::mode_range(md)]) << 6 | cem[0] << 12 | shared << 16;
     }
     return AKV_SUCCESS;
 }

@@ -64,7 +64,7 @@ constexpr uint32_t kInfoIdentity = 1u << 24;
 constexpr uint32_t kInfoTable = 1u << 25;
 
 template <int NCH>
-struct alignas(8) BlockDesc {
+struct BlockDesc {
     static constexpr int kTabEntries = 32 / NCH;   // 64 bytes of FP16 texel values
     union {
         uint32_t ep[4][NCH];   // compute path: e0 | e1 << 16 (UNORM16) per partition and channel
@@ -73,8 +73,9 @@ struct alignas(8) BlockDesc {
     uint32_t qw[5];            // weight fields, nb bits each, grid order (planes interleaved); qw[4] = 0
     uint32_t part[4];          // 2-bit partition index per texel (texel i: word i / 16, bits 2 * (i % 16))
     uint32_t info;
+    uint32_t pad;              // 27 dwords: consecutive records start in different LDS banks
 };
-static_assert(sizeof(BlockDesc<4>) == 104 && sizeof(BlockDesc<1>) == 104, "BlockDesc layout");
+static_assert(sizeof(BlockDesc<4>) == 108 && sizeof(BlockDesc<1>) == 108, "BlockDesc layout");
 
 struct Footprint {
     int bx, by, ntex, ds, dt;   // ds, dt: weight infill steps (1024 + b/2) / (b - 1)
@@ -310,7 +311,7 @@ __device__ __attribute__((always_inline)) inline void weight_fields(const uint32
 // from bit `start` of the block `blk` (four words in LDS) -> cv (packed bytes).
 __device__ __attribute__((always_inline)) inline void decode_colour_values(const uint32_t* blk, int start, int crange, int nv, const LdsTables& L,
                                             uint32_t* cv) {
-    const uint4 b4 = *reinterpret_cast<const uint4*>(blk);
+    const uint4 b4 = uint4{blk[0], blk[1], blk[2], blk[3]};   // records are 4-byte aligned
     while (true) {
         const int r = __builtin_amdgcn_readfirstlane(crange);
         if (crange == r) {
@@ -356,7 +357,7 @@ template <bool CAP>
 __device__ __attribute__((always_inline)) inline void decode_weight_fields(const uint32_t* rev, int wrange, int wbits,
                                                                            int count, const LdsTables& L,
                                                                            uint32_t (&q)[5]) {
-    const uint4 r4 = *reinterpret_cast<const uint4*>(rev);
+    const uint4 r4 = uint4{rev[0], rev[1], rev[2], rev[3]};
     const int key = CAP ? (wrange | ((count <= 16 ? 0 : count <= 36 ? 1 : 2) << 4)) : wrange;
     while (true) {
         const int rk = __builtin_amdgcn_readfirstlane(key);
@@ -592,10 +593,14 @@ struct FieldWriter {
 // writes it (block_part_words) any time before the texel stage.
 template <int NCH>
 __device__ inline void stash_block(BlockDesc<NCH>& d, uint4 raw) {
-    uint4* t = reinterpret_cast<uint4*>(d.tab);
-    t[0] = raw;
-    t[2] = uint4{__builtin_bitreverse32(raw.w), __builtin_bitreverse32(raw.z), __builtin_bitreverse32(raw.y),
-                 __builtin_bitreverse32(raw.x)};
+    d.tab[0] = raw.x;
+    d.tab[1] = raw.y;
+    d.tab[2] = raw.z;
+    d.tab[3] = raw.w;
+    d.tab[8] = __builtin_bitreverse32(raw.w);
+    d.tab[9] = __builtin_bitreverse32(raw.z);
+    d.tab[10] = __builtin_bitreverse32(raw.y);
+    d.tab[11] = __builtin_bitreverse32(raw.x);
     d.tab[12] = 0;
 }
 
@@ -834,7 +839,7 @@ __device__ inline uint2 texel_fp16(const BlockDesc<NCH>& d, const LdsTables& L, 
     if (info & kInfoTable) {
         const uint32_t nb = (info >> kInfoNbShift) & 7;
         const int entry = p * int((info >> kInfoLevelsShift) & 63) + int(field_at(d, nb, i));
-        if constexpr (NCH == 4) return *reinterpret_cast<const uint2*>(&d.tab[2 * entry]);
+        if constexpr (NCH == 4) return uint2{d.tab[2 * entry], d.tab[2 * entry + 1]};
         else return uint2{reinterpret_cast<const uint16_t*>(d.tab)[entry], 0u};
     }
     return texel_compute<NCH>(d, L, f.bx, f.ds, f.dt, x, y, p);
@@ -863,7 +868,7 @@ __device__ inline void texels_fp16(const BlockDesc<NCH>* desc, const int (&blk)[
         const BlockDesc<NCH>& d = desc[blk[k]];
         const uint32_t nb = (info[k] >> kInfoNbShift) & 7;
         const int entry = int(__umul24(uint32_t(p[k]), (info[k] >> kInfoLevelsShift) & 63)) + int(field_at(d, nb, i[k]));
-        if constexpr (NCH == 4) out[k] = *reinterpret_cast<const uint2*>(&d.tab[2 * entry]);
+        if constexpr (NCH == 4) out[k] = uint2{d.tab[2 * entry], d.tab[2 * entry + 1]};
         else out[k] = uint2{reinterpret_cast<const uint16_t*>(d.tab)[entry], 0u};
         all_table = all_table && (info[k] & kInfoTable);
     }

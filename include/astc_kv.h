@@ -62,6 +62,17 @@ int akv_encode_blocks(void* ctx, const float* texels, size_t n, uint8_t* blocks)
 int akv_decode_blocks_fp16(unsigned bx, unsigned by, const uint8_t* blocks, size_t n, uint16_t* texels,
                            int32_t* kinds);
 
+/* akv_block_classes: the decode-path class of each of n blocks of a bx x by
+   footprint (what decides its decode cost), one word per block:
+   bits 0-1 kind (AKV_CLASS_NORMAL / VOID / ERROR, by the same rules as
+   akv_decode_blocks_fp16's kinds), 2-3 partitions - 1, 4 dual plane,
+   5 weight grid the size of the block, 6-11 weight levels, 12-15 endpoint
+   mode of the first partition, 16 one endpoint mode shared by every
+   partition. The normal-block fields are zero for void-extent and error
+   blocks. No counterpart in the reference: a diagnostic for atlases. */
+enum { AKV_CLASS_NORMAL = 0, AKV_CLASS_VOID = 1, AKV_CLASS_ERROR = 2 };
+int akv_block_classes(unsigned bx, unsigned by, const uint8_t* blocks, size_t n, uint32_t* out);
+
 #ifdef __cplusplus
 }
 #endif

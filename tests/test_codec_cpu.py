@@ -283,3 +283,35 @@ def test_default_tiles():
     assert tile_for_splits(2048, 8, 6, 64) == 256 and -(-2048 // 256) == 8
     p = fp16_params(16, 3, 9, 8192, 64)
     assert p.tile_tokens == 512 and p.splits == 16
+
+
+@pytest.mark.parametrize("bx,by", [(4, 4), (6, 5), (6, 6), (8, 8)])
+def test_block_classes_against_oracle_kinds_and_spec_fields(bx, by):
+    """akv_block_classes: the kind of every block equals the oracle decoder's
+    (void extents valid and invalid included), and each normal block's fields
+    equal those the spec-written parser reads from it."""
+    import astc_spec as S
+    from astc_kv.atlas import block_class_histogram
+    from test_oracle_reductions import constructed_blocks
+    rng = np.random.default_rng(bx * 31 + by)
+    rand = rng.integers(0, 256, size=(20000, 16), dtype=np.uint8)
+    rand[:1000, 0] = 0xFC
+    rand[:1000, 1] = (rand[:1000, 1] & 0xF0) | rng.choice([0x0D, 0x0F], size=1000).astype(np.uint8)
+    rand[:200, 8:] = 0xFF   # all-ones extents
+    blocks = np.concatenate([np.array(constructed_blocks(bx, by), np.uint8).reshape(-1, 16), rand])
+    lib = codec.load_codec_library()
+    cls = np.empty(len(blocks), np.uint32)
+    assert lib.akv_block_classes(bx, by, blocks.ctypes.data, len(blocks), cls.ctypes.data) == 0
+    _, kinds = O.decode_blocks_fp16(blocks, bx, by)
+    np.testing.assert_array_equal(cls & 3, kinds)
+    assert np.count_nonzero(kinds == 0) > 400 and np.count_nonzero(kinds == 1) > 100
+    for raw, c in zip(blocks[kinds == 0], cls[kinds == 0]):
+        b = S.parse_block(bytes(raw))
+        shared = len(b.cems) == 1 or (raw[2] >> 7 | (raw[3] & 1) << 1) == 0   # bits 23-24
+        expect = ((len(b.cems) - 1) << 2 | b.dual << 4 | int((b.w, b.h) == (bx, by)) << 5 |
+                  S.LEVELS[b.wrange] << 6 | b.cems[0] << 12 | int(shared) << 16)
+        assert int(c) == expect, (raw.tolist(), hex(int(c)), hex(expect))
+    h = block_class_histogram(blocks, bx, by, "rgba")
+    assert h["blocks"] == len(blocks)
+    assert abs(h["table_path"] + h["compute_path"] + h["void_extent"] + h["error"] - 1) < 1e-3
+    assert abs(sum(h["partitions"].values()) - np.mean(kinds == 0)) < 1e-3
