@@ -24,7 +24,7 @@ the HIP path:
                  (:719-725).
 
 Only then are `rounds` x `iterations` steps timed with HIP events.
-`python -m astc_kv.probe MANIFEST [--tile T] [--rounds R] [--iterations N]`
+`python -m astc_kv.probe MANIFEST [--tile T] [--tokens T] [--rounds R] [--iterations N]`
 prints one JSON object; the exit status is 0, 1 for a refusal and 2 for a
 fixture this path does not run (the reference's v10 probe takes FP16 K and
 token-normalised ASTC V only, :460-461).
@@ -68,6 +68,35 @@ def load_fixture(manifest: Path) -> dict:
         if name:
             fx[f"{side}_decoded"] = np.fromfile(d / name, "<f4").reshape(1, hkv, t, dim)
     return fx
+
+
+def repeat_tokens(fx: dict, tokens: int) -> dict:
+    """The fixture repeated along the sequence to `tokens` keys, as the
+    reference builds its traffic controls (scripts/make_traffic_fixture.py:
+    12-49): token i of K, its offline decode, V's offline decode and V's
+    scale/offset is source token i mod T; ASTC block row r is source row
+    r mod (T / block height), for as many rows as `tokens` rounded up to whole
+    pages; the query is unchanged. Bounded to 1..8192 tokens like the
+    reference's. Timing on such a fixture measures shape and traffic only."""
+    from .atlas import Atlas
+    if not 1 <= tokens <= 8192:
+        raise ValueError("repeated fixtures are bounded to 1..8192 tokens")
+    a = fx["atlas"]
+    t = a.tokens
+    if t % a.block_y or a.rows != t // a.block_y:
+        raise ValueError("the source fixture must hold whole block rows of its tokens")
+    idx = np.arange(tokens) % t
+    padded = -(-tokens // a.page_tokens) * a.page_tokens
+    rows = np.arange(-(-padded // a.block_y)) % a.rows
+    atlas = Atlas(np.ascontiguousarray(a.blocks[:, :, rows]), np.ascontiguousarray(a.scale[..., idx]),
+                  np.ascontiguousarray(a.offset[..., idx]), tokens, a.dim, a.layout, a.block_x, a.block_y,
+                  a.page_tokens)
+    out = dict(fx, atlas=atlas, k=np.ascontiguousarray(fx["k"][:, :, idx]),
+               manifest=dict(fx["manifest"], tokens=tokens, source_tokens=t))
+    for side in ("v_decoded", "k_decoded"):
+        if fx[side] is not None:
+            out[side] = np.ascontiguousarray(fx[side][:, :, idx])
+    return out
 
 
 def attention_fp64(q, k, v):
@@ -145,8 +174,10 @@ def refusal(correctness: dict) -> dict:
     return {"schema": SCHEMA_FAIL, "status": "correctness_failed", "correctness": correctness, "raw_samples": []}
 
 
-def run(manifest: Path, tile: int | None = None, rounds: int = 5, iterations: int = 20) -> tuple[int, dict]:
-    """Gates, then timing. Returns (exit status, JSON record)."""
+def run(manifest: Path, tile: int | None = None, rounds: int = 5, iterations: int = 20,
+        tokens: int | None = None) -> tuple[int, dict]:
+    """Gates, then timing; `tokens` repeats the fixture to that many keys
+    first (repeat_tokens). Returns (exit status, JSON record)."""
     import torch
 
     from . import gpu
@@ -154,6 +185,8 @@ def run(manifest: Path, tile: int | None = None, rounds: int = 5, iterations: in
         fx = load_fixture(manifest)
     except UnsupportedFixture as e:
         return 2, {"schema": SCHEMA_FAIL, "status": "unsupported_fixture", "error": str(e), "raw_samples": []}
+    if tokens:
+        fx = repeat_tokens(fx, tokens)
     atlas = gpu.DeviceAtlas.from_host(fx["atlas"])
     qt = torch.from_numpy(fx["q"]).cuda()
     kt = torch.from_numpy(fx["k"]).cuda()
@@ -180,7 +213,8 @@ def run(manifest: Path, tile: int | None = None, rounds: int = 5, iterations: in
         t1.record(stream)
         t1.synchronize()
         samples.append(t0.elapsed_time(t1) * 1e3 / iterations)
-    return 0, {"schema": SCHEMA_OK, "status": "ok", "correctness": correctness, "tile_tokens": params.tile_tokens,
+    return 0, {"schema": SCHEMA_OK, "status": "ok", "correctness": correctness, "tokens": fx["atlas"].tokens,
+               "tile_tokens": params.tile_tokens,
                "splits": params.splits, "raw_samples": samples, "median_us": float(np.median(samples)),
                "unit": "us per decode-attention step (one launch)"}
 
@@ -191,8 +225,10 @@ def main(argv=None) -> int:
     ap.add_argument("--tile", type=int, default=None, help="tokens per split (any positive count)")
     ap.add_argument("--rounds", type=int, default=5)
     ap.add_argument("--iterations", type=int, default=20)
+    ap.add_argument("--tokens", type=int, default=None,
+                    help="repeat the fixture's blocks to this many keys (1..8192) before running")
     a = ap.parse_args(argv)
-    rc, record = run(a.manifest, a.tile, a.rounds, a.iterations)
+    rc, record = run(a.manifest, a.tile, a.rounds, a.iterations, a.tokens)
     print(json.dumps(record, indent=1))
     if rc == 1:
         print("astc-kv probe: attention correctness gate failed; no timing result is published", file=sys.stderr)

@@ -62,6 +62,11 @@ constexpr int kInfoRangeShift = 14;             // bits 14-17: weight range
 constexpr int kInfoLevelsShift = 18;            // bits 18-23: table row length (weight levels)
 constexpr uint32_t kInfoIdentity = 1u << 24;
 constexpr uint32_t kInfoTable = 1u << 25;
+// A reduced weight grid with one plane, whose texel weights a fill stage
+// (fill_weights) infills once per chunk: texel i's weight (0..64) is byte i
+// from dword (bits 27-31) of the record on, just past the endpoint pairs.
+constexpr uint32_t kInfoFilled = 1u << 26;
+constexpr int kInfoFillShift = 27;
 
 template <int NCH>
 struct BlockDesc {
@@ -643,9 +648,13 @@ __device__ inline uint4 block_part_words(uint4 raw, uint4 words) {
 // `cv` is this lane's scratch for the unquantised colour values
 // (kColourScratchWords dwords, four values per dword).
 // Every table read is from LDS.
-template <int NCH, bool CAP = false>
+// With FILL, a reduced single-plane grid whose `ntex` texel weights fit
+// after its endpoint pairs in the endpoint/table union and the weight fields
+// (84 bytes) is marked kInfoFilled: the caller then runs fill_weights on it
+// before the texel stage.
+template <int NCH, bool CAP = false, bool FILL = false>
 __device__ __attribute__((always_inline)) inline void decode_header(const LdsTables& L, BlockDesc<NCH>& d,
-                                                                   uint32_t* cv) {
+                                                                   uint32_t* cv, int ntex = 0) {
     const uint32_t* blk = d.tab;        // block bits
     const uint32_t* rev = d.tab + 8;    // weight stream
     const uint32_t w0 = blk[0];
@@ -762,9 +771,12 @@ __device__ __attribute__((always_inline)) inline void decode_header(const LdsTab
             for (int ch = 0; ch < NCH; ++ch) d.ep[p][ch] = ep[ch];
         }
     }
+    const int woff = parts * NCH;   // dwords of endpoint pairs
+    const bool fill = FILL && !identity && !dual && 4 * woff + ntex <= 84;
     d.info = (md & 0xFFu) | (dual ? kInfoDual : 0u) | (ccs << 9) | (uint32_t(nb) << kInfoNbShift) |
              (uint32_t(wrange) << kInfoRangeShift) | (uint32_t(levels) << kInfoLevelsShift) |
-             (identity ? kInfoIdentity : 0u) | (table ? kInfoTable : 0u);
+             (identity ? kInfoIdentity : 0u) | (table ? kInfoTable : 0u) |
+             (fill ? kInfoFilled | (uint32_t(woff) << kInfoFillShift) : 0u);
 }
 
 // Weight field `idx` (grid order, planes interleaved) of a block.
@@ -829,6 +841,45 @@ __device__ inline uint2 texel_identity(const BlockDesc<NCH>& d, const LdsTables&
     else return uint2{pack_fp16_rtz(C[0], kCBias) & 0xFFFFu, 0u};
 }
 
+// Stage 1b: the texel weights of the kInfoFilled blocks `list[0..n)`, by
+// whole waves, one lane per texel: a wave takes 64 / span blocks per pass
+// (span: the texel count rounded up to 16, 32 or 64, so ntex <= 64). Each
+// lane writes its texel's weight byte over the block's endpoint/table union
+// and weight fields, which the other lanes of the same block read: the
+// block's lanes are one wave's, and a lane's store depends on its own loads,
+// so the wave's loads have all returned when its first store issues. A
+// workgroup barrier must follow before the texel stage.
+template <int NCH, int NT>
+__device__ inline void fill_weights(BlockDesc<NCH>* desc, const LdsTables& L, Footprint f, const uint8_t* list, int n,
+                                    int tid) {
+    const int span = f.ntex <= 16 ? 16 : f.ntex <= 32 ? 32 : 64;
+    const int per = 64 / span;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int sub = lane / span, t = lane & (span - 1);
+    const int y = int((float(t) + 0.5f) * (1.0f / float(f.bx)));   // t < 64, bx <= 12: exact
+    const int x = t - y * f.bx;
+    for (int base = wave * per; base < n; base += (NT / 64) * per) {
+        const int e = base + sub;
+        if (e < n && t < f.ntex) {
+            BlockDesc<NCH>& d = desc[list[e]];
+            const uint32_t info = d.info;
+            const int w = texel_weight(d, L, f.bx, f.ds, f.dt, info, x, y, 0);
+            reinterpret_cast<uint8_t*>(d.tab)[4 * int(info >> kInfoFillShift) + t] = uint8_t(w);
+        }
+    }
+}
+
+// Stage 2 of a kInfoFilled block: the weight byte, then the interpolation.
+template <int NCH>
+__device__ inline uint2 texel_filled(const BlockDesc<NCH>& d, uint32_t info, int i, int p) {
+    const uint32_t wp = weight_pair(int(reinterpret_cast<const uint8_t*>(d.tab)[4 * int(info >> kInfoFillShift) + i]));
+    uint32_t C[NCH];
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) C[ch] = interp_c(d.ep[p][ch], wp);
+    if constexpr (NCH == 4) return uint2{pack_fp16_rtz(C[0], C[1]), pack_fp16_rtz(C[2], C[3])};
+    else return uint2{pack_fp16_rtz(C[0], kCBias) & 0xFFFFu, 0u};
+}
+
 // Stage 2: the FP16 values of texel (x, y) of a block (NCH == 4:
 // {R | G << 16, B | A << 16}; NCH == 1: R in the low half of .x).
 template <int NCH>
@@ -876,7 +927,9 @@ __device__ inline void texels_fp16(const BlockDesc<NCH>* desc, const int (&blk)[
 #pragma unroll
         for (int k = 0; k < K; ++k)
             if (!(info[k] & kInfoTable)) {
-                if (NCH == 4 && (info[k] & (kInfoIdentity | kInfoDual)) == kInfoIdentity)
+                if (info[k] & kInfoFilled)
+                    out[k] = texel_filled<NCH>(desc[blk[k]], info[k], i[k], p[k]);
+                else if (NCH == 4 && (info[k] & (kInfoIdentity | kInfoDual)) == kInfoIdentity)
                     out[k] = texel_identity<NCH>(desc[blk[k]], L, info[k], i[k], p[k]);
                 else
                     out[k] = texel_compute<NCH>(desc[blk[k]], L, f.bx, f.ds, f.dt, x[k], y[k], p[k]);

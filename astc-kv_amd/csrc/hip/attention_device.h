@@ -551,12 +551,14 @@ struct AstcShared {
         struct {
             BlockDesc<NCH> desc[C::kMaxBlocks];
             uint32_t cv[C::kMaxBlocks][kColourScratchWords];   // header-stage colour values, per lane
+            uint8_t fill[C::kMaxBlocks];                       // blocks for the fill stage (kInfoFilled)
         } h;
         float comb[kWaves * D * kMaxG];      // final per-wave accumulators
     } u;
     uint32_t so[C::kMaxTok];                 // per-token V scale | offset << 16 (fp16)
     uint32_t tokrow[C::kMaxTok];             // token_row_entry of each chunk token
     uint32_t key_count[kPathKeys];           // blocks per decode-path class (zero between chunks)
+    uint32_t nfill;                          // entries of u.h.fill (zero between chunks)
     uint8_t order[C::kMaxBlocks];            // blocks sorted by decode-path class
     uint2 q[2 * C::kKSteps][64];             // Q operands (fp16 high, low)
     WaveStats ws;

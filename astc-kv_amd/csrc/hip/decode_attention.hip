@@ -86,14 +86,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
     if constexpr (!DUMP)
         if (wave == 0) qst.store(a.qscale, &sh.q[0][0]);
     if (tid < kPathKeys) sh.key_count[tid] = 0;
+    if (tid == 0) sh.nfill = 0;
 
-    // This lane's texel columns: x = n16 + 16 * kc -> block column and x in block.
-    int bcol[C::kColGroups], xin[C::kColGroups];
+    // This lane's texel columns: x = n16 + 16 * kc -> block column | x in
+    // block << 16 (one register each).
+    int colpk[C::kColGroups];
 #pragma unroll
     for (int kc = 0; kc < C::kColGroups; ++kc) {
         const int x = n16 + 16 * kc;
-        bcol[kc] = int(fdiv(uint32_t(x), a.mag_bx));
-        xin[kc] = x - bcol[kc] * f.bx;
+        const int bc = int(fdiv(uint32_t(x), a.mag_bx));
+        colpk[kc] = bc | ((x - bc * f.bx) << 16);
     }
 
     AttnState<D> st;
@@ -157,10 +159,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
             for (int t = kKEarly; t < TPG; ++t)
                 load_k_tile<D>(kreg + t * C::kRowLoads, krs, 16 * (TPG * wave + t), lane);
         }
-        if (tid < nblk) decode_header<NCH, D == 128>(sh.tabs, sh.u.h.desc[sh.order[tid]], sh.u.h.cv[tid]);
-        // What the texel stage needs besides the headers: each lane's own
-        // block's partition words, and the per-token scale | offset << 16
-        // (zero past the chunk, up to the tile edge).
+        // What the texel stage needs besides the headers, written first so
+        // that nothing of it stays in registers through the header stage:
+        // each lane's own block's partition words (a field the header stage
+        // does not touch), and the per-token scale | offset << 16 (zero past
+        // the chunk, up to the tile edge).
         if (tid < nblk) {
             const uint4 w = block_part_words(raw_now, pat);
             uint32_t* part = sh.u.h.desc[tid].part;   // 4-byte aligned
@@ -176,7 +179,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
                 if (t < 16 * ntiles) sh.so[t] = t < ntok ? sc[i] | (of[i] << 16) : 0u;
             }
         }
+        if (tid < nblk) {
+            const int bi = sh.order[tid];
+            decode_header<NCH, D == 128, true>(sh.tabs, sh.u.h.desc[bi], sh.u.h.cv[tid], f.ntex);
+            if (sh.u.h.desc[bi].info & kInfoFilled) sh.u.h.fill[atomicAdd(&sh.nfill, 1u)] = uint8_t(bi);
+        }
         __syncthreads();
+        // 2b. Reduced weight grids: every texel weight infilled once, by whole
+        // waves, rather than at each texel lookup.
+        if (const int nfill = __builtin_amdgcn_readfirstlane(int(sh.nfill))) {
+            fill_weights<NCH, kThreads>(sh.u.h.desc, sh.tabs, f, sh.u.h.fill, nfill, tid);
+            __syncthreads();
+            if (tid == 0) sh.nfill = 0;   // read by every thread before the barrier above
+        }
         // 3. This wave's groups of TPG consecutive tiles (every fourth group):
         // S for the whole group, then for each tile its texels straight into
         // MFMA operands and P.V. The next group's K rows are requested as soon
@@ -189,7 +204,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
 #pragma unroll
                 for (int kc = 0; kc < C::kColGroups; ++kc) {
                     uint2 tv[4];
-                    column_texels<NCH>(sh.u.h.desc, sh.tabs, f, rows, bcol[kc], xin[kc], tv);
+                    column_texels<NCH>(sh.u.h.desc, sh.tabs, f, rows, colpk[kc] & 0xFFFF, colpk[kc] >> 16, tv);
                     const int x = n16 + 16 * kc;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -217,7 +232,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
                             tile_rows(sh.tokrow, tb0 + 16 * t, g, rows);
                         }
                         uint2 tv[4];
-                        column_texels<NCH>(sh.u.h.desc, sh.tabs, f, rows, bcol[kc], xin[kc], tv);
+                        column_texels<NCH>(sh.u.h.desc, sh.tabs, f, rows, colpk[kc] & 0xFFFF, colpk[kc] >> 16, tv);
                         texel_operands<NCH>(tv, va);
                     });
             }

@@ -151,13 +151,15 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
     tables.store(sh.tabs, tid);
     if (wave == 0) qst.store(a.qscale, &sh.q[0][0]);
     if (tid < kPathKeys) sh.key_count[tid] = 0;
+    if (tid == 0) sh.nfill = 0;
 
-    int bcol[C::kColGroups], xin[C::kColGroups];
+    // (block column | x in block << 16, one register each).
+    int colpk[C::kColGroups];
 #pragma unroll
     for (int kc = 0; kc < C::kColGroups; ++kc) {
         const int x = n16 + 16 * kc;
-        bcol[kc] = int(fdiv(uint32_t(x), a.mag_bx));
-        xin[kc] = x - bcol[kc] * f.bx;
+        const int bc = int(fdiv(uint32_t(x), a.mag_bx));
+        colpk[kc] = bc | ((x - bc * f.bx) << 16);
     }
 
     AttnState<D> st;
@@ -240,10 +242,11 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
         place_by_class(sh.key_count, sh.order, key, rank, tid < nblk, tid);
         __syncthreads();   // sorted order complete (and every count read)
         if (wave == 0) sh.key_count[lane] = 0;   // for the next chunk (two barriers away)
-        if (tid < nblk) decode_header<NCH>(sh.tabs, sh.u.h.desc[sh.order[tid]], sh.u.h.cv[tid]);
-        // Each lane's own block's partition words, and the per-token scale |
-        // offset << 16 (tail tokens: fp16 1.0 and 0; zero past the chunk, up
-        // to the tile edge).
+        // Each lane's own block's partition words (a field the header stage
+        // does not touch), and the per-token scale | offset << 16 (tail
+        // tokens: fp16 1.0 and 0; zero past the chunk, up to the tile edge),
+        // written first so that nothing of them stays in registers through
+        // the header stage.
         if (tid < nblk) {
             const uint4 w = block_part_words(raw_now, pat);
             uint32_t* part = sh.u.h.desc[tid].part;   // 4-byte aligned
@@ -257,7 +260,19 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
             const int t = tid + i * kThreads;
             if (t < 16 * ntiles) sh.so[t] = t >= ntok ? 0u : c0 + t < full ? sc[i] | (of[i] << 16) : 0x3C00u;
         }
+        if (tid < nblk) {
+            const int bi = sh.order[tid];
+            decode_header<NCH, false, true>(sh.tabs, sh.u.h.desc[bi], sh.u.h.cv[tid], f.ntex);
+            if (sh.u.h.desc[bi].info & kInfoFilled) sh.u.h.fill[atomicAdd(&sh.nfill, 1u)] = uint8_t(bi);
+        }
         __syncthreads();
+        // 2b. Reduced weight grids: every texel weight infilled once, by whole
+        // waves, rather than at each texel lookup.
+        if (const int nfill = __builtin_amdgcn_readfirstlane(int(sh.nfill))) {
+            fill_weights<NCH, kThreads>(sh.u.h.desc, sh.tabs, f, sh.u.h.fill, nfill, tid);
+            __syncthreads();
+            if (tid == 0) sh.nfill = 0;   // read by every thread before the barrier above
+        }
         // 3. Tile groups; tiles at or past `full` read V from the FP16 tail.
 #pragma unroll
         for (int t = kKEarly; t < TPG; ++t) load_k(kw + t * kKWords, c0, 16 * (TPG * wave + t));
@@ -284,7 +299,7 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
                 }
                 uint2 tv[4];
                 if (in_tail) tail_texels<D, NCH>(tail, trow, n16 + 16 * kc, tv);
-                else column_texels<NCH>(sh.u.h.desc, sh.tabs, f, rows, bcol[kc], xin[kc], tv);
+                else column_texels<NCH>(sh.u.h.desc, sh.tabs, f, rows, colpk[kc] & 0xFFFF, colpk[kc] >> 16, tv);
                 texel_operands<NCH>(tv, va);
             };
             if constexpr (KU4)

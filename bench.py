@@ -3,21 +3,35 @@
 
 Workload (one step = one decode step of the whole batch): T=8192 keys per
 sequence, batch 16, 9 query heads / 3 KV heads, head dim 64, FP16 K, V as an
-ASTC RGBA 6x5 atlas (page 120) with per-token fp16 scale/offset; independent
-seeded K/V per sequence (K ~ N(0,1) with 4 channels x8, V ~ N(0, 0.5), q ~ N(0,1)).
+ASTC RGBA 6x5 atlas (page 120) with per-token fp16 scale/offset, encoded at
+quality 98 (the reference bridge's default, astc_kv/codec.py:116-117);
+independent seeded K/V per sequence (K ~ N(0,1) with 4 channels x8,
+V ~ N(0, 0.5), q ~ N(0,1)). The same workload encoded at quality 50 is timed
+beside it (`quality_50`), and each atlas's block classes are reported
+(`v_blocks`: table-path / compute-path fractions, partitions, weight levels,
+endpoint modes), since the decode cost depends on them.
 
 Inputs are resident in HBM. A pool of distinct copies of the KV set (> 512 MB
 in total) is rotated across steps so that the 256 MB Infinity Cache cannot
-hold the working set; every step is timed as split + merge launches replayed
-from a HIP graph, with events on the launch stream.
+hold the working set; every step is timed as one launch (split kernel with the
+merge in its last workgroup per head) replayed from a HIP graph, with events
+on the launch stream. `copy_ceiling` is a device-to-device copy timed the
+same way (what the box sustains for read + write).
 
 Prints one JSON line. `value` is the effective bandwidth: algorithmic bytes
 of a step (K + ASTC blocks read + V scale/offset + q + out) / step time.
-`roofline.achieved` is the split kernel's algorithmic bytes (K + ASTC blocks
-+ V scale/offset + q) / its own launch time. `roofline.traffic` is the HBM
-traffic per split launch that rocprofv3 measured (FETCH_SIZE + WRITE_SIZE,
-scaled by a plain copy kernel of known size) for this same workload, read from
-the committed profile summary when its workload line matches.
+`roofline.achieved` is the same bytes over the same one-launch time.
+`roofline.traffic` is the HBM traffic per launch that rocprofv3 measured
+(FETCH_SIZE + WRITE_SIZE, scaled by a plain copy kernel of known size) for
+this same workload, read from the committed profile summary whose workload
+line matches.
+
+`--fixture DIR` times the reference's own astcenc payload fixture instead,
+repeated to --tokens keys as the reference's traffic controls are
+(scripts/make_traffic_fixture.py:12-49), batch 1, at the host's tile and at
+the reference's tile for that size, next to the reference's published M5 Pro
+times for the same payloads (docs/research_v3_report.md:28-32).
+`--ragged N` times a paged ragged batch with block tables.
 
 `python bench.py --summarize KT FETCH WRITE` instead prints a markdown summary
 of rocprofv3 CSV output directories (kernel trace with --stats, a FETCH_SIZE
@@ -65,7 +79,15 @@ def parse_args(argv=None):
     ap.add_argument("--page", type=int, default=120)
     ap.add_argument("--tile", type=int, default=0, help="tokens per split (0 = automatic)")
     ap.add_argument("--fp16-tile", type=int, default=0, help="tokens per split of the FP16 control (0 = automatic)")
-    ap.add_argument("--quality", type=float, default=50.0, help="encoder effort for the synthetic V atlas")
+    ap.add_argument("--quality", type=float, default=98.0, help="encoder effort for the synthetic V atlas")
+    ap.add_argument("--compare-quality", type=float, default=50.0,
+                    help="also time the same workload encoded at this quality (0: off)")
+    ap.add_argument("--fixture", default=None,
+                    help="time an astc-kv-probe-v1 fixture directory (e.g. tests/golden/t384) repeated to --tokens")
+    ap.add_argument("--ref-tile", type=int, default=0,
+                    help="fixture: the reference's tile for this size (0: its protocol's 32/64/256 at T384/2048/8192)")
+    ap.add_argument("--copy-ceiling-mb", type=float, default=1024.0,
+                    help="size of the device-to-device copy timed for the copy ceiling (0: off)")
     ap.add_argument("--pool-mb", type=float, default=600.0, help="minimum bytes of distinct KV sets rotated")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget")
     ap.add_argument("--no-cpu", action="store_true")
@@ -80,6 +102,8 @@ def parse_args(argv=None):
     ap.add_argument("--summarize", nargs=3, metavar=("KT", "FETCH", "WRITE"),
                     help="print a markdown summary of rocprofv3 CSV output directories and exit")
     ap.add_argument("--out", default="", help="also write the JSON line to this file")
+    ap.add_argument("--k-dist", default="outlier", choices=["outlier", "t3"],
+                    help="K ~ N(0,1) with 4 channels x8, or Student-t with 3 degrees of freedom")
     ap.add_argument("--ragged", type=int, default=0,
                     help="paged ragged batch of this many sequences (lengths uniform in "
                          "[--min-tokens, --tokens]) instead of the uniform batch")
@@ -89,10 +113,60 @@ def parse_args(argv=None):
     return ap.parse_args(argv)
 
 
-def workload_name(a) -> str:
+def workload_name(a, quality=None) -> str:
     bx, by = a.block.split("x")
-    return (f"decode attention T{a.tokens} batch {a.batch}, {a.query_heads}q/{a.kv_heads}kv, D{a.dim}, "
-            f"FP16 K + ASTC {a.layout.upper()} {bx}x{by} V (page {a.page})")
+    kd = ", Student-t K" if a.k_dist == "t3" else ""
+    return (f"decode attention T{a.tokens} batch {a.batch}, {a.query_heads}q/{a.kv_heads}kv, D{a.dim}{kd}, "
+            f"FP16 K + ASTC {a.layout.upper()} {bx}x{by} V (page {a.page}, quality {a.quality if quality is None else quality:g})")
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def copy_ceiling(torch, mb: float, reps: int = 20) -> dict | None:
+    """Device-to-device copy of `mb` MB (read mb, write mb), timed with events
+    on the current stream: the read + write rate the box sustains."""
+    if mb <= 0:
+        return None
+    n = int(mb * 1e6) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    stream = torch.cuda.current_stream()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for _ in range(reps):
+        dst.copy_(src)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / reps
+    del src, dst
+    gbs = 2 * n * 4 / (ms * 1e-3) / 1e9
+    return {"GB/s": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes_moved": 2 * n * 4,
+            "us": round(ms * 1e3, 2), "kernel": "torch copy_ (float32, device to device)"}
+
+
+def byte_ratios(a, nbytes) -> dict:
+    """Persistent K + V + V metadata bytes over FP16 K + FP16 V for this
+    workload, and for the same shape with a scalar 6x6 V atlas (the
+    reference's compact layout; its T8192 measurement is 3,981,312 /
+    6,291,456 = 0.6328, docs/research_v4_report.md:71-75)."""
+    fp16 = 2 * nbytes["k"]
+    per_tok_scalar66 = -(-a.dim // 6) * 16 / 6
+    b, h, t = a.batch, a.kv_heads, a.tokens
+    scalar = nbytes["k"] + b * h * (-(-t // 6) * 6) * per_tok_scalar66 + nbytes["v_meta"]
+    return {"kv_over_fp16": round((nbytes["k"] + nbytes["v_blocks"] + nbytes["v_meta"]) / fp16, 4),
+            "v_over_fp16_v": round((nbytes["v_blocks"] + nbytes["v_meta"]) / nbytes["k"], 4),
+            "scalar6x6_kv_over_fp16": round(scalar / fp16, 4)}
 
 
 def make_inputs(a, rng_seed=20261201):
@@ -103,8 +177,11 @@ def make_inputs(a, rng_seed=20261201):
     for s in range(b):
         rng = np.random.default_rng(rng_seed + s)
         q[s] = rng.normal(size=(hq, d))
-        ks = rng.normal(size=(hkv, t, d))
-        ks[..., :4] *= 8.0
+        if a.k_dist == "t3":
+            ks = rng.standard_t(3, size=(hkv, t, d))
+        else:
+            ks = rng.normal(size=(hkv, t, d))
+            ks[..., :4] *= 8.0
         k[s] = ks
         v[s] = rng.normal(0.0, 0.5, size=(hkv, t, d))
     return q, k, v
@@ -309,14 +386,56 @@ def ragged_workload_name(a) -> str:
     bx, by = a.block.split("x")
     return (f"paged decode attention, ragged batch of {a.ragged} (T uniform in [{a.min_tokens},{a.tokens}]), "
             f"{a.query_heads}q/{a.kv_heads}kv, D{a.dim}, {a.k_format} K + ASTC {a.layout.upper()} {bx}x{by} V "
-            f"(page {a.page}{', FP16 tail' if a.tail else ''}), block tables")
+            f"(page {a.page}{', FP16 tail' if a.tail else ''}, quality {a.quality:g}), block tables")
+
+
+def seq_bytes(pk, i) -> int:
+    """Algorithmic bytes a decode step reads for sequence i of a paged cache
+    (the per-sequence terms of PagedKV.byte_counts)."""
+    n, full, h, d = int(pk.seq_lens[i]), pk.full_tokens(i), pk.kv_heads, pk.dim
+    k = h * n * (d * 2 if pk.k_format == "fp16" else d // 2 + (d // 32) * 4)
+    return k + h * -(-full // pk.block_y) * pk.cols * 16 + h * full * 4 + h * (n - full) * d * 2
+
+
+def cpu_leg_ragged(q, kv, seconds, sample_bytes, what):
+    """The oracle's NumPy attention per sequence of a sample (K, V float32
+    [Hkv, T, D] each), all host cores then one."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import attention_ref as R
+    cores = len(os.sched_getaffinity(0))
+
+    def once():
+        for i, (k, v) in enumerate(kv):
+            R.decode_attention(q[i:i + 1], k[None], v[None])
+
+    res = {}
+    for n, budget in ((cores, seconds * 0.6), (1, seconds * 0.4)):
+        with threadpool_limits(limits=n):
+            once()
+            times = []
+            start = time.perf_counter()
+            while (time.perf_counter() - start < budget and len(times) < 200) or len(times) < 3:
+                t0 = time.perf_counter()
+                once()
+                times.append(time.perf_counter() - t0)
+        res[n] = (float(np.median(times)), len(times))
+    sec, sec1 = res[cores][0], res[1][0]
+    return {"value": round(sample_bytes / sec / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": f"{what}: median of {res[cores][1]} passes of the oracle's NumPy attention "
+                      f"(astc_kv/codec.py:253-267) per sequence on pre-decoded K and V, {sec * 1e6:.0f} us per pass "
+                      f"on {cores} cores ({sec1 * 1e6:.0f} us on 1 core); GB/s over the sample's algorithmic bytes",
+            "us_per_sample": round(sec * 1e6, 1), "us_per_sample_1core": round(sec1 * 1e6, 1),
+            "sample_bytes": int(sample_bytes)}
 
 
 def main_ragged(a, torch, gpu):
     """A ragged batch in page pools with block tables (akv_hip_paged_decode_attention)."""
+    from astc_kv.atlas import block_class_histogram
     from astc_kv.paged import build_paged
-    from oracle import astc_oracle as O
     from oracle import attention_ref as R
+    from oracle.paged_ref import host_kv
 
     bx, by = (int(x) for x in a.block.split("x"))
     rng = np.random.default_rng(20261202)
@@ -352,39 +471,34 @@ def main_ragged(a, torch, gpu):
     log(f"timing {a.steps} steps (tile {params.tile_tokens}, {s} splits max)")
     ms_step, mode = time_graph(torch, step, a.steps, a.warmup, not a.no_graph)
 
+    ceiling = copy_ceiling(torch, a.copy_ceiling_mb)
     # Parity on the shortest and the longest sequence.
     step(0)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     sub = [int(np.argmin(lens)), int(np.argmax(lens))]
     max_err, parity = 0.0, True
+    host = {}
     for i in sub:
-        t, P, h, d = lens[i], a.page, a.kv_heads, a.dim
-        ids = pk.block_table[i, :-(-t // P)]
-        if a.k_format == "fp16":
-            ki = pk.k_pages[ids].transpose(1, 0, 2, 3).reshape(h, -1, d)[:, :t].astype(np.float32)
-        else:
-            kb = pk.k_pages[ids].transpose(1, 0, 2, 3).reshape(h, -1, d // 2)[:, :t]
-            codes = np.stack([kb & 15, kb >> 4], -1).reshape(h, t, d // 32, 32).astype(np.float32)
-            meta = pk.k_meta[ids].transpose(1, 0, 2, 3, 4).reshape(h, -1, d // 32, 2)[:, :t].astype(np.float32)
-            ki = (codes * meta[..., 1:2] + meta[..., 0:1]).reshape(h, t, d)
-        full = pk.full_tokens(i)
-        parts = []
-        if full:
-            npg, rpp, cols = -(-full // P), P // by, pk.cols
-            blocks = pk.v_blocks[ids[:npg]].transpose(1, 0, 2, 3, 4).reshape(h, npg * rpp, cols, 16)
-            tex, _ = O.decode_blocks_fp16(np.ascontiguousarray(blocks).reshape(-1, 16), bx, by)
-            img = tex.reshape(h, npg * rpp, cols, by, bx, 4).transpose(0, 1, 3, 2, 4, 5)
-            img = img.reshape(h, npg * P, cols * bx, 4)[:, :full].astype(np.float32)
-            u = img[..., :d, 0] if a.layout == "scalar" else img[:, :, : d // 4].reshape(h, full, d)
-            sc = pk.v_scale[ids[:npg]].transpose(1, 0, 2).reshape(h, -1)[:, :full].astype(np.float32)
-            of = pk.v_offset[ids[:npg]].transpose(1, 0, 2).reshape(h, -1)[:, :full].astype(np.float32)
-            parts.append(R.restore_token(u, sc[..., None], of[..., None]))
-        if full < t:
-            parts.append(pk.v_tail[i, :, : t - full].astype(np.float32))
-        ref = R.decode_attention(q[i:i + 1], ki[None], np.concatenate(parts, 1)[None])[0]
+        host[i] = host_kv(pk, i)
+        ref = R.decode_attention(q[i:i + 1], host[i][0][None], host[i][1][None])[0]
         max_err = max(max_err, float(np.max(np.abs(got[i] - ref))))
         parity = parity and bool(np.allclose(got[i], ref, rtol=1e-3, atol=2e-3))
+
+    cpu = None
+    if not a.no_cpu:
+        # A bounded sample: the first sequences of the batch up to about 64k
+        # tokens, K and V pre-decoded on the host, one NumPy attention each.
+        n_s, tok = 0, 0
+        while n_s < len(lens) and (tok < 65536 or n_s == 0):
+            tok += lens[n_s]
+            n_s += 1
+        log(f"timing the CPU baseline on {n_s} sequences ({tok} tokens)")
+        kv = [host.get(i) or host_kv(pk, i) for i in range(n_s)]
+        sample_bytes = sum(seq_bytes(pk, i) + 2 * a.query_heads * a.dim * 4 for i in range(n_s))
+        cpu = cpu_leg_ragged(q[:n_s], kv, a.cpu_seconds, sample_bytes,
+                             f"the first {n_s} sequences of the batch ({tok} of {sum(lens)} tokens)")
+        del kv
 
     value = step_bytes_ / (ms_step * 1e-3) / 1e9
     line = {
@@ -404,16 +518,172 @@ def main_ragged(a, torch, gpu):
                      "traffic_source": traffic["source"] if traffic else None,
                      "kernel": "paged_attn_kernel (split + in-kernel merge)", "bytes_per_launch": step_bytes_,
                      "us_per_launch": round(ms_step * 1e3, 3)},
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
+        "v_blocks": block_class_histogram(pk.v_blocks[np.unique(np.concatenate(
+            [pk.block_table[i, :-(-pk.full_tokens(i) // a.page)] for i in range(a.ragged)]))], bx, by, a.layout),
+        "copy_ceiling": ceiling,
         "parity": {"sequences_checked": sub, "max_abs_err": max_err, "within_rtol1e-3_atol2e-3": parity},
         "setup_s": round(setup_s, 2),
     }
+    emit(a, line)
+    return 0 if parity else 1
+
+
+def oracle_values(atlas, sub):
+    """V of sequences `sub` restored on the host from the oracle's decode of
+    their blocks (float32 [len(sub), Hkv, T, D])."""
+    from astc_kv.atlas import Atlas
+    from oracle import astc_oracle as O
+    from oracle import attention_ref as R
+    bx, by = atlas.block_x, atlas.block_y
+    small = Atlas(atlas.blocks[sub], atlas.scale[sub], atlas.offset[sub], atlas.tokens, atlas.dim, atlas.layout,
+                  bx, by, atlas.page_tokens)
+    tex, _ = O.decode_blocks_fp16(small.blocks.reshape(-1, 16), bx, by)
+    bb, hh, rr, cc = small.blocks.shape[:4]
+    img = tex.reshape(bb, hh, rr, cc, by, bx, 4).transpose(0, 1, 2, 4, 3, 5, 6).reshape(bb, hh, rr * by, cc * bx, 4)
+    img = img[:, :, : atlas.tokens].astype(np.float32)
+    d = atlas.dim
+    un = img[..., :d, 0] if atlas.layout == "scalar" else img[:, :, :, : d // 4].reshape(bb, hh, atlas.tokens, d)
+    return R.restore_token(un, small.scale.astype(np.float32)[..., None], small.offset.astype(np.float32)[..., None])
+
+
+def time_atlas(a, torch, gpu, qt, kt, dev, params, steps, warmup):
+    """(pooled ms per step, resident ms per step, pool size) of the one-launch
+    decode step over `dev`."""
+    s = params.splits
+    partial = torch.empty((a.batch, a.query_heads, s, a.dim), dtype=torch.float32, device="cuda")
+    stats = torch.empty((a.batch, a.query_heads, s, 2), dtype=torch.float32, device="cuda")
+    out = torch.empty((a.batch, a.query_heads, a.dim), dtype=torch.float32, device="cuda")
+    set_bytes = kt.numel() * 2 + dev.nbytes() + qt.numel() * 4
+    pool_n = max(1, int(np.ceil(a.pool_mb * 1e6 / set_bytes)))
+    pool = [(kt, dev)] + [(kt.clone(), dev.clone()) for _ in range(pool_n - 1)]
+
+    def step(i):
+        kk, dd = pool[i % pool_n]
+        gpu.decode_attention(qt, kk, dd, params=params, partial=partial, stats=stats, out=out)
+
+    torch.cuda.synchronize()
+    ms_step, mode = time_graph(torch, step, steps, warmup, not a.no_graph)
+
+    def resident(i):
+        gpu.decode_attention(qt, kt, dev, params=params, partial=partial, stats=stats, out=out)
+
+    ms_resident, _ = time_graph(torch, resident, steps, warmup, not a.no_graph)
+    del pool
+    return ms_step, ms_resident, pool_n, mode
+
+
+def cpu_leg(q, k, v_rest, seconds, step_bytes_, what):
+    """The oracle's NumPy attention timed on the host cores (all, then one)."""
+    sec, cores, sec1, reps = cpu_baseline(q, k, v_rest, seconds)
+    return {"value": round(step_bytes_ / sec / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": f"{what}: median of {reps} steps of the oracle's NumPy attention (astc_kv/codec.py:253-267) "
+                      f"on pre-decoded V, {sec * 1e6:.0f} us/step on {cores} cores ({sec1 * 1e6:.0f} us/step on "
+                      f"1 core)",
+            "us_per_step": round(sec * 1e6, 1), "us_per_step_1core": round(sec1 * 1e6, 1)}
+
+
+def emit(a, line) -> None:
     text = json.dumps(line)
     print(text, flush=True)
     if a.out:
         Path(a.out).parent.mkdir(parents=True, exist_ok=True)
         Path(a.out).write_text(text + "\n")
-    return 0 if parity else 1
+
+
+REFERENCE_TILES = {384: 32, 2048: 64, 8192: 256}           # configs/address_v7_20261029.json
+REFERENCE_M5PRO_US = {384: (7.842, 5.733), 2048: (16.014, 11.738), 8192: (39.659, 25.337)}   # v7 hoisted, own FP16
+
+
+def fixture_workload_name(a, m) -> str:
+    return (f"reference fixture {Path(a.fixture).name} ({m['encoder']['name']} {m['encoder']['version']} "
+            f"quality {m['encoder']['quality']:g}, {m['layout']} ASTC {a.block}, page {a.page}) repeated to "
+            f"T{a.tokens}, batch 1, {m['query_heads']}q/{m['kv_heads']}kv, D{m['head_dim']}, FP16 K")
+
+
+def main_fixture(a, torch, gpu):
+    """The reference's own astcenc payloads (an astc-kv-probe-v1 fixture),
+    repeated to a.tokens keys, through the probe's correctness gates, then
+    timed at the host's tile and at the reference's."""
+    from astc_kv import probe
+    from astc_kv.atlas import block_class_histogram
+    fx = probe.load_fixture(Path(a.fixture) / "manifest.json")
+    if a.tokens != fx["atlas"].tokens:
+        fx = probe.repeat_tokens(fx, a.tokens)
+    m = fx["manifest"]
+    atlas = fx["atlas"]
+    dev = gpu.DeviceAtlas.from_host(atlas)
+    qt = torch.from_numpy(fx["q"]).cuda()
+    kt = torch.from_numpy(fx["k"]).cuda()
+    a.batch, a.query_heads, a.kv_heads, a.dim = 1, m["query_heads"], m["kv_heads"], m["head_dim"]
+    a.layout, a.block, a.page = atlas.layout, f"{atlas.block_x}x{atlas.block_y}", atlas.page_tokens
+    ref_tile = a.ref_tile or REFERENCE_TILES.get(a.tokens)
+    # Gates first, as the reference's probe does (probe_gqa_v10.mm:704-784).
+    params = gpu.make_params(dev, a.query_heads, a.tile or None)
+    u = gpu.decode_values(dev, params.tile_tokens)
+    v_restored = (u.float() * dev.scale.float()[..., None]) + dev.offset.float()[..., None]
+    out = gpu.decode_attention(qt, kt, dev, params=params)
+    out16 = gpu.fp16_attention(qt, kt, v_restored.half(), fused=False)
+    torch.cuda.synchronize()
+    passed, correctness = probe.gates(fx, v_restored.cpu().numpy(), out.cpu().numpy(), out16.cpu().numpy())
+    if not passed:
+        emit(a, probe.refusal(correctness))
+        return 1
+    nbytes = step_bytes(a, atlas)
+    runs = {}
+    for name, tile in (("host_tile", a.tile or None), ("reference_tile", ref_tile)):
+        if tile is None and name == "reference_tile":
+            continue
+        p = gpu.make_params(dev, a.query_heads, tile)
+        ms, ms_res, pool_n, mode = time_atlas(a, torch, gpu, qt, kt, dev, p, a.steps, a.warmup)
+        runs[name] = {"tile_tokens": p.tile_tokens, "splits": p.splits, "us_per_step": round(ms * 1e3, 3),
+                      "us_per_step_resident": round(ms_res * 1e3, 3), "pool_sets": pool_n,
+                      "GB/s": round(nbytes["step"] / (ms * 1e-3) / 1e9, 2)}
+    fparams = gpu.fp16_params(1, a.kv_heads, a.query_heads, a.tokens, a.dim, ref_tile)
+    v16 = v_restored.half()
+    fpart = torch.empty((1, a.query_heads, fparams.splits, a.dim), dtype=torch.float32, device="cuda")
+    fstat = torch.empty_like(fpart[..., :2])
+
+    def fstep(i):
+        gpu.fp16_attention(qt, kt, v16, params=fparams, partial=fpart, stats=fstat, out=out, fused=False)
+
+    ms_fp16, _ = time_graph(torch, fstep, a.steps, a.warmup, not a.no_graph)
+    best = min(runs.values(), key=lambda r: r["us_per_step"])
+    ms_step = best["us_per_step"] * 1e-3
+    value = nbytes["step"] / (ms_step * 1e-3) / 1e9
+    published = REFERENCE_M5PRO_US.get(a.tokens)
+    cpu = None
+    if not a.no_cpu:
+        cpu = cpu_leg(fx["q"], fx["k"], v_restored.cpu().numpy(), a.cpu_seconds, nbytes["step"],
+                      f"the whole fixture step (batch 1, T{a.tokens})")
+    line = {
+        "metric": "µs per decode-attention step + effective KV GB/s (% HBM peak)",
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 6), "us_per_step": best["us_per_step"],
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp16 K / ASTC V (u16 texels), fp32 accumulate",
+        "data": f"the reference's {m['model']} layer {m['layer']} capture, {m['encoder']['name']} "
+                f"{m['encoder']['version']} payloads, repeated (synthetic traffic control, not quality evidence)",
+        "config": {"workload": fixture_workload_name(a, m), "tokens": a.tokens, "source_tokens": m.get(
+                   "source_tokens", a.tokens), "layout": a.layout, "block": [atlas.block_x, atlas.block_y],
+                   "timing": "hipgraph" if not a.no_graph else "eager", "bytes_per_step": nbytes},
+        "runs": runs,
+        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "astc_attn_kernel (split + in-kernel merge, ASTC V)",
+                     "bytes_per_launch": nbytes["step"], "us_per_launch": best["us_per_step"],
+                     "note": "launch-latency bound at these sizes; the fraction is not meaningful below ~1 MB"},
+        "fp16_control": {"us_per_step": round(ms_fp16 * 1e3, 3), "tile_tokens": fparams.tile_tokens},
+        "reference_m5pro_us": None if published is None else {
+            "astc_v7_hoisted": published[0], "fp16_own": published[1],
+            "source": "docs/research_v3_report.md:28-32 (medians of session medians, warm, one resident cache)"},
+        "v_blocks": block_class_histogram(atlas.blocks, atlas.block_x, atlas.block_y, atlas.layout),
+        "correctness": correctness,
+        "cpu_baseline": cpu,
+    }
+    emit(a, line)
+    return 0
 
 
 def main(argv=None):
@@ -432,9 +702,11 @@ def main(argv=None):
     import torch
 
     from astc_kv import gpu
+    if a.fixture:
+        return main_fixture(a, torch, gpu)
     if a.ragged:
         return main_ragged(a, torch, gpu)
-    from astc_kv.atlas import Atlas, build_atlas
+    from astc_kv.atlas import block_class_histogram, build_atlas
     from oracle import astc_oracle as O
     from oracle import attention_ref as R
 
@@ -444,36 +716,35 @@ def main(argv=None):
     q, k, v = make_inputs(a)
     atlas = build_atlas(v, a.layout, (bx, by), a.page, a.quality)
     setup_s = time.perf_counter() - t_setup
+    atlas_cmp = None
+    if a.compare_quality > 0 and a.compare_quality != a.quality:
+        log(f"encoding the comparison atlas at quality {a.compare_quality:g}")
+        atlas_cmp = build_atlas(v, a.layout, (bx, by), a.page, a.compare_quality)
+    del v
     dev = gpu.DeviceAtlas.from_host(atlas)
     qt = torch.from_numpy(q).cuda()
     kt = torch.from_numpy(k).cuda()
     params = gpu.make_params(dev, a.query_heads, a.tile or None)
     nbytes = step_bytes(a, atlas)
-    set_bytes = kt.numel() * 2 + dev.nbytes() + qt.numel() * 4
-    pool_n = max(1, int(np.ceil(a.pool_mb * 1e6 / set_bytes)))
-    pool = [(kt, dev)] + [(kt.clone(), dev.clone()) for _ in range(pool_n - 1)]
-    s = params.splits
-    partial = torch.empty((a.batch, a.query_heads, s, a.dim), dtype=torch.float32, device="cuda")
-    stats = torch.empty((a.batch, a.query_heads, s, 2), dtype=torch.float32, device="cuda")
     out = torch.empty((a.batch, a.query_heads, a.dim), dtype=torch.float32, device="cuda")
 
     if a.copy_calibration_mb > 0:
         copy_calibration(torch, a.copy_calibration_mb)
 
-    # One launch per step: the split kernel with the merge done by the last
-    # split workgroup of each (sequence, kv head).
-    def step(i):
-        kk, dd = pool[i % pool_n]
-        gpu.decode_attention(qt, kk, dd, params=params, partial=partial, stats=stats, out=out)
+    log(f"timing {a.steps} steps (tile {params.tile_tokens}, {params.splits} splits)")
+    ms_step, ms_resident, pool_n, mode = time_atlas(a, torch, gpu, qt, kt, dev, params, a.steps, a.warmup)
 
-    torch.cuda.synchronize()
-    log(f"timing {a.steps} steps (tile {params.tile_tokens}, {s} splits, pool of {pool_n} KV sets)")
-    ms_step, mode = time_graph(torch, step, a.steps, a.warmup, not a.no_graph)
-
-    def resident(i):
-        gpu.decode_attention(qt, kt, dev, params=params, partial=partial, stats=stats, out=out)
-
-    ms_resident, _ = time_graph(torch, resident, a.steps, a.warmup, not a.no_graph)
+    cmp = None
+    if atlas_cmp is not None:
+        log(f"timing the quality {a.compare_quality:g} atlas")
+        dev_c = gpu.DeviceAtlas.from_host(atlas_cmp)
+        ms_c, ms_c_res, _, _ = time_atlas(a, torch, gpu, qt, kt, dev_c, params, a.steps, a.warmup)
+        cmp = {"quality": a.compare_quality, "us_per_step": round(ms_c * 1e3, 3),
+               "us_per_step_resident": round(ms_c_res * 1e3, 3),
+               "GB/s": round(nbytes["step"] / (ms_c * 1e-3) / 1e9, 2),
+               "frac": round(nbytes["step"] / (ms_c * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+               "v_blocks": block_class_histogram(atlas_cmp.blocks, bx, by, a.layout)}
+        del dev_c
 
     # FP16 K/V control on the same workload (V = restored values rounded to fp16).
     log("timing the FP16-K/V control")
@@ -494,21 +765,16 @@ def main(argv=None):
 
     ms_fp16, _ = time_graph(torch, fstep, a.steps, a.warmup, not a.no_graph)
     fp16_bytes = nbytes["k"] * 2 + nbytes["q"] + nbytes["out"]
-    del fpool
+    del fpool, v16
+    ceiling = copy_ceiling(torch, a.copy_ceiling_mb)
 
     # Correctness of the measured configuration on two sequences (oracle decode + NumPy attention).
     log("checking two sequences against the oracle")
-    step(0)
+    gpu.decode_attention(qt, kt, dev, params=params, out=out)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     sub = [0, a.batch - 1]
-    small = Atlas(atlas.blocks[sub], atlas.scale[sub], atlas.offset[sub], a.tokens, a.dim, a.layout, bx, by, a.page)
-    tex, _ = O.decode_blocks_fp16(small.blocks.reshape(-1, 16), bx, by)
-    bb, hh, rr, cc = small.blocks.shape[:4]
-    img = tex.reshape(bb, hh, rr, cc, by, bx, 4).transpose(0, 1, 2, 4, 3, 5, 6).reshape(bb, hh, rr * by, cc * bx, 4)
-    img = img[:, :, : a.tokens].astype(np.float32)
-    un = img[..., : a.dim, 0] if a.layout == "scalar" else img[:, :, :, : a.dim // 4].reshape(bb, hh, a.tokens, a.dim)
-    vr = R.restore_token(un, small.scale.astype(np.float32)[..., None], small.offset.astype(np.float32)[..., None])
+    vr = oracle_values(atlas, sub)
     ref = R.decode_attention(q[sub], k[sub].astype(np.float32), vr)
     max_err = float(np.max(np.abs(got[sub] - ref)))
     parity = bool(np.allclose(got[sub], ref, rtol=1e-3, atol=2e-3))
@@ -517,26 +783,15 @@ def main(argv=None):
     if not a.no_cpu:
         log("timing the CPU baseline (oracle decode + NumPy attention)")
         t0 = time.perf_counter()
-        tex_all, _ = O.decode_blocks_fp16(atlas.blocks.reshape(-1, 16), bx, by)
+        O.decode_blocks_fp16(atlas.blocks.reshape(-1, 16), bx, by)
         decode_s = time.perf_counter() - t0
-        bb, hh, rr, cc = atlas.blocks.shape[:4]
-        img = tex_all.reshape(bb, hh, rr, cc, by, bx, 4).transpose(0, 1, 2, 4, 3, 5, 6)
-        img = img.reshape(bb, hh, rr * by, cc * bx, 4)[:, :, : a.tokens].astype(np.float32)
-        un = img[..., : a.dim, 0] if a.layout == "scalar" else img[:, :, :, : a.dim // 4].reshape(
-            bb, hh, a.tokens, a.dim)
-        v_rest = R.restore_token(un, atlas.scale.astype(np.float32)[..., None],
-                                 atlas.offset.astype(np.float32)[..., None])
-        del tex_all, img, un
-        sec, cores, sec1, reps = cpu_baseline(q, k, v_rest, a.cpu_seconds)
-        cpu = {"value": round(nbytes["step"] / sec / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-               "sample": f"full workload (batch {a.batch}, T{a.tokens}): median of {reps} steps of the oracle's "
-                         f"NumPy attention (astc_kv/codec.py:253-267) on pre-decoded V, {sec*1e6:.0f} us/step on "
-                         f"{cores} cores ({sec1*1e6:.0f} us/step on 1 core); the oracle's single-threaded C ASTC "
-                         f"decode of the whole atlas took {decode_s*1e6:.0f} us more, not folded in",
-               "us_per_step": round(sec * 1e6, 1), "us_per_step_1core": round(sec1 * 1e6, 1),
-               "astc_decode_us_1core": round(decode_s * 1e6, 1)}
+        v_rest = oracle_values(atlas, list(range(a.batch)))
+        cpu = cpu_leg(q, k, v_rest, a.cpu_seconds, nbytes["step"], f"full workload (batch {a.batch}, T{a.tokens})")
+        cpu["sample"] += (f"; the oracle's single-threaded C ASTC decode of the whole atlas took "
+                          f"{decode_s * 1e6:.0f} us more, not folded in")
+        cpu["astc_decode_us_1core"] = round(decode_s * 1e6, 1)
+        del v_rest
 
-    achieved = nbytes["step"] / (ms_step * 1e-3) / 1e9
     value = nbytes["step"] / (ms_step * 1e-3) / 1e9
     traffic = read_traffic(a.traffic, workload_name(a))
     line = {
@@ -553,32 +808,32 @@ def main(argv=None):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16 K / ASTC V (u16 texels), fp32 accumulate",
-        "data": "synthetic (seeded Gaussian K/V/q), V encoded by this package's ASTC encoder",
+        "data": f"synthetic (seeded Gaussian K/V/q), V encoded by this package's ASTC encoder at quality "
+                f"{a.quality:g}",
         "config": {"workload": workload_name(a),
                    "batch": a.batch, "tokens": a.tokens, "query_heads": a.query_heads, "kv_heads": a.kv_heads,
-                   "dim": a.dim, "layout": a.layout, "block": [bx, by], "tile_tokens": params.tile_tokens,
-                   "splits": params.splits, "pool_sets": pool_n, "timing": mode,
-                   "bytes_per_step": nbytes},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                   "dim": a.dim, "layout": a.layout, "block": [bx, by], "quality": a.quality,
+                   "tile_tokens": params.tile_tokens, "splits": params.splits, "pool_sets": pool_n,
+                   "timing": mode, "bytes_per_step": nbytes, "byte_ratios": byte_ratios(a, nbytes)},
+        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4),
                      "traffic": traffic["bytes"] if traffic else None,
                      "traffic_source": traffic["source"] if traffic else None,
                      "kernel": "astc_attn_kernel (split + in-kernel merge, ASTC V)",
                      "bytes_per_launch": nbytes["step"], "us_per_launch": round(ms_step * 1e3, 3)},
         "cpu_baseline": cpu,
+        "v_blocks": block_class_histogram(atlas.blocks, bx, by, a.layout),
+        "quality_50" if a.compare_quality == 50 else "quality_compare": cmp,
         "resident_single_set": {"us_per_step": round(ms_resident * 1e3, 3),
                                 "GB/s": round(nbytes["step"] / (ms_resident * 1e-3) / 1e9, 2)},
         "fp16_control": {"us_per_step": round(ms_fp16 * 1e3, 3), "bytes_per_step": fp16_bytes,
                          "GB/s": round(fp16_bytes / (ms_fp16 * 1e-3) / 1e9, 2), "tile_tokens": fparams.tile_tokens,
                          "astc_speedup": round(ms_fp16 / ms_step, 4)},
+        "copy_ceiling": ceiling,
         "parity": {"sequences_checked": sub, "max_abs_err": max_err, "within_rtol1e-3_atol2e-3": parity},
         "setup_s": round(setup_s, 2),
     }
-    text = json.dumps(line)
-    print(text, flush=True)
-    if a.out:
-        Path(a.out).parent.mkdir(parents=True, exist_ok=True)
-        Path(a.out).write_text(text + "\n")
+    emit(a, line)
     return 0 if parity else 1
 
 

@@ -93,7 +93,7 @@ def _paged_case(gpu, rng):
 
 
 def _paged_ref(pk, q, i):
-    from test_gpu_paged import host_kv
+    from oracle.paged_ref import host_kv
     ki, vi = host_kv(pk, i)
     return R.decode_attention(q[i:i + 1], ki[None], vi[None])[0]
 

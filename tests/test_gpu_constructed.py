@@ -130,7 +130,7 @@ def test_attention_over_random_blocks(gpu, layout, block, dim, hq, hkv):
 
 def test_paged_attention_over_random_v_blocks(gpu):
     from astc_kv.paged import build_paged
-    from test_gpu_paged import host_kv
+    from oracle.paged_ref import host_kv
     rng = np.random.default_rng(77)
     lens = [700, 130, 1000, 96]
     k = [rng.normal(size=(2, t, 128)).astype(np.float16) for t in lens]

@@ -80,7 +80,7 @@ def test_t8192_b16_9q3kv_d64_rgba4x4(gpu):
 
 def test_ragged64_d128_u4k_scalar6x6_paged(gpu):
     from astc_kv.paged import build_paged
-    from test_gpu_paged import host_kv
+    from oracle.paged_ref import host_kv
     t0 = time.time()
     rng = np.random.default_rng(20261202)
     lens = rng.integers(512, 16384 + 1, size=64).tolist()

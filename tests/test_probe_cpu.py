@@ -67,3 +67,29 @@ def test_fp64_reference_matches_codec_attention(fixture):
     v, out, _ = _standins(fixture)
     ref = probe.attention_fp64(fixture["q"][0], fixture["k"][0], v[0])
     np.testing.assert_allclose(out[0], ref, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("tokens", [391, 2048, 8192])
+def test_repeated_fixture(fixture, tokens):
+    """A fixture repeated to T keys (the reference's traffic controls,
+    scripts/make_traffic_fixture.py:12-49): block rows cover T rounded up to
+    whole pages, the decoded atlas is the offline decode repeated token by
+    token, and the gates still pass on it."""
+    fx = probe.repeat_tokens(fixture, tokens)
+    a = fx["atlas"]
+    assert a.tokens == tokens and fx["k"].shape[2] == tokens and fx["v_decoded"].shape[2] == tokens
+    assert a.rows == -(-tokens // a.page_tokens) * a.page_tokens // a.block_y
+    r = np.arange(a.rows) % fixture["atlas"].rows
+    assert np.array_equal(a.blocks, fixture["atlas"].blocks[:, :, r])
+    v = a.restored().astype(np.float32)
+    assert np.array_equal(v.view(np.uint32), fx["v_decoded"].view(np.uint32))
+    if tokens <= 2048:
+        v, out, out16 = _standins(fx)
+        passed, c = probe.gates(fx, v, out, out16)
+        assert passed, c
+
+
+def test_repeated_fixture_bounds(fixture):
+    for bad in (0, 8193):
+        with pytest.raises(ValueError):
+            probe.repeat_tokens(fixture, bad)
