@@ -220,12 +220,13 @@ int decode_block_unorm16(const AkvTables& t, const uint8_t* block, uint16_t* tex
     ise_unpack(t, b, color_start, 2 * pairs, crange, vals);
     for (int i = 0; i < 2 * pairs; ++i) vals[i] = t.color_unq[crange][vals[i]];
     // 16-bit endpoints (e8 * 257) and LDR flags per partition.
-    int e0[4][4], e1[4][4];
+    // (HDR endpoint modes leave their endpoints unset: error texels.)
+    int e0[4][4] = {}, e1[4][4] = {};
     bool ldr[4];
     for (int p = 0, k = 0; p < parts; ++p) {
         ldr[p] = ldr_endpoints(cem[p], vals + k, e0[p], e1[p]);
         k += 2 * ((cem[p] >> 2) + 1);
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < 4 && ldr[p]; ++c) {
             e0[p][c] *= 257;
             e1[p][c] *= 257;
         }

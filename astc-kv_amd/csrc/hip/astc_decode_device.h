@@ -901,7 +901,8 @@ __device__ inline uint2 texel_fp16(const BlockDesc<NCH>& d, const LdsTables& L, 
 // together), and the compute path runs only where a block needs it. The
 // table read of a block that is not a table may land anywhere in the first
 // kilobyte past its record (entry < 128); its value is replaced.
-template <int NCH, int K>
+// FILL: the kernel runs the fill stage (kInfoFilled blocks are filled).
+template <int NCH, int K, bool FILL>
 __device__ inline void texels_fp16(const BlockDesc<NCH>* desc, const int (&blk)[K], const int (&i)[K],
                                    const int (&x)[K], const int (&y)[K], const LdsTables& L, Footprint f,
                                    uint2 (&out)[K]) {
@@ -927,7 +928,7 @@ __device__ inline void texels_fp16(const BlockDesc<NCH>* desc, const int (&blk)[
 #pragma unroll
         for (int k = 0; k < K; ++k)
             if (!(info[k] & kInfoTable)) {
-                if (info[k] & kInfoFilled)
+                if (FILL && (info[k] & kInfoFilled))
                     out[k] = texel_filled<NCH>(desc[blk[k]], info[k], i[k], p[k]);
                 else if (NCH == 4 && (info[k] & (kInfoIdentity | kInfoDual)) == kInfoIdentity)
                     out[k] = texel_identity<NCH>(desc[blk[k]], L, info[k], i[k], p[k]);

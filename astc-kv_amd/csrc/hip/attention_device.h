@@ -586,7 +586,7 @@ __device__ inline void tile_rows(const uint32_t* tokrow, int t0, int g, uint32_t
 
 // Texels of one texel column (block column bcol, x = xin in the block) for
 // the four tokens of `rows`.
-template <int NCH>
+template <int NCH, bool FILL>
 __device__ __attribute__((always_inline)) inline void column_texels(const BlockDesc<NCH>* desc, const LdsTables& L,
                                                                     Footprint f, const uint32_t (&rows)[4], int bcol,
                                                                     int xin, uint2 (&tv)[4]) {
@@ -598,7 +598,7 @@ __device__ __attribute__((always_inline)) inline void column_texels(const BlockD
         xk[tk] = xin;
         yk[tk] = int(rows[tk] & 0xFF);
     }
-    texels_fp16<NCH, 4>(desc, bk, ik, xk, yk, L, f, tv);
+    texels_fp16<NCH, 4, FILL>(desc, bk, ik, xk, yk, L, f, tv);
 }
 
 // Row table of a chunk: token t -> (first block of its block row) << 16 |

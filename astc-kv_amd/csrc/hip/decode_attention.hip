@@ -204,7 +204,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
 #pragma unroll
                 for (int kc = 0; kc < C::kColGroups; ++kc) {
                     uint2 tv[4];
-                    column_texels<NCH>(sh.u.h.desc, sh.tabs, f, rows, colpk[kc] & 0xFFFF, colpk[kc] >> 16, tv);
+                    column_texels<NCH, true>(sh.u.h.desc, sh.tabs, f, rows, colpk[kc] & 0xFFFF, colpk[kc] >> 16, tv);
                     const int x = n16 + 16 * kc;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -232,7 +232,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
                             tile_rows(sh.tokrow, tb0 + 16 * t, g, rows);
                         }
                         uint2 tv[4];
-                        column_texels<NCH>(sh.u.h.desc, sh.tabs, f, rows, colpk[kc] & 0xFFFF, colpk[kc] >> 16, tv);
+                        column_texels<NCH, true>(sh.u.h.desc, sh.tabs, f, rows, colpk[kc] & 0xFFFF, colpk[kc] >> 16, tv);
                         texel_operands<NCH>(tv, va);
                     });
             }

@@ -151,7 +151,6 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
     tables.store(sh.tabs, tid);
     if (wave == 0) qst.store(a.qscale, &sh.q[0][0]);
     if (tid < kPathKeys) sh.key_count[tid] = 0;
-    if (tid == 0) sh.nfill = 0;
 
     // (block column | x in block << 16, one register each).
     int colpk[C::kColGroups];
@@ -262,17 +261,9 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
         }
         if (tid < nblk) {
             const int bi = sh.order[tid];
-            decode_header<NCH, false, true>(sh.tabs, sh.u.h.desc[bi], sh.u.h.cv[tid], f.ntex);
-            if (sh.u.h.desc[bi].info & kInfoFilled) sh.u.h.fill[atomicAdd(&sh.nfill, 1u)] = uint8_t(bi);
+            decode_header<NCH>(sh.tabs, sh.u.h.desc[bi], sh.u.h.cv[tid]);
         }
         __syncthreads();
-        // 2b. Reduced weight grids: every texel weight infilled once, by whole
-        // waves, rather than at each texel lookup.
-        if (const int nfill = __builtin_amdgcn_readfirstlane(int(sh.nfill))) {
-            fill_weights<NCH, kThreads>(sh.u.h.desc, sh.tabs, f, sh.u.h.fill, nfill, tid);
-            __syncthreads();
-            if (tid == 0) sh.nfill = 0;   // read by every thread before the barrier above
-        }
         // 3. Tile groups; tiles at or past `full` read V from the FP16 tail.
 #pragma unroll
         for (int t = kKEarly; t < TPG; ++t) load_k(kw + t * kKWords, c0, 16 * (TPG * wave + t));
@@ -299,7 +290,7 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
                 }
                 uint2 tv[4];
                 if (in_tail) tail_texels<D, NCH>(tail, trow, n16 + 16 * kc, tv);
-                else column_texels<NCH>(sh.u.h.desc, sh.tabs, f, rows, colpk[kc] & 0xFFFF, colpk[kc] >> 16, tv);
+                else column_texels<NCH, false>(sh.u.h.desc, sh.tabs, f, rows, colpk[kc] & 0xFFFF, colpk[kc] >> 16, tv);
                 texel_operands<NCH>(tv, va);
             };
             if constexpr (KU4)

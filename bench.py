@@ -102,6 +102,9 @@ def parse_args(argv=None):
     ap.add_argument("--summarize", nargs=3, metavar=("KT", "FETCH", "WRITE"),
                     help="print a markdown summary of rocprofv3 CSV output directories and exit")
     ap.add_argument("--out", default="", help="also write the JSON line to this file")
+    ap.add_argument("--cache", default="",
+                    help="directory for the encoded V atlases / paged pools of these arguments (reused when present)")
+    ap.add_argument("--no-resident", action="store_true", help="skip the single-set (cache-resident) timing")
     ap.add_argument("--k-dist", default="outlier", choices=["outlier", "t3"],
                     help="K ~ N(0,1) with 4 channels x8, or Student-t with 3 degrees of freedom")
     ap.add_argument("--ragged", type=int, default=0,
@@ -118,6 +121,31 @@ def workload_name(a, quality=None) -> str:
     kd = ", Student-t K" if a.k_dist == "t3" else ""
     return (f"decode attention T{a.tokens} batch {a.batch}, {a.query_heads}q/{a.kv_heads}kv, D{a.dim}{kd}, "
             f"FP16 K + ASTC {a.layout.upper()} {bx}x{by} V (page {a.page}, quality {a.quality if quality is None else quality:g})")
+
+
+def _cache_path(a, what: str) -> Path | None:
+    """Cache file of an encoded input: the arguments that fix it, hashed."""
+    if not a.cache:
+        return None
+    import hashlib
+    key = json.dumps([what, a.batch, a.tokens, a.query_heads, a.kv_heads, a.dim, a.layout, a.block, a.page,
+                      a.k_dist, a.ragged, a.min_tokens, a.k_format, a.tail], sort_keys=True)
+    return Path(a.cache) / f"{what}-{hashlib.sha256(key.encode()).hexdigest()[:16]}.npz"
+
+
+def cached_atlas(a, v, quality):
+    """build_atlas, or the atlas a previous run with the same arguments saved."""
+    from astc_kv.atlas import Atlas, build_atlas
+    bx, by = (int(x) for x in a.block.split("x"))
+    path = _cache_path(a, f"atlas-q{quality:g}")
+    if path is not None and path.exists():
+        z = np.load(path)
+        return Atlas(z["blocks"], z["scale"], z["offset"], a.tokens, a.dim, a.layout, bx, by, a.page)
+    atlas = build_atlas(v, a.layout, (bx, by), a.page, quality)
+    if path is not None:
+        path.parent.mkdir(parents=True, exist_ok=True)
+        np.savez(path, blocks=atlas.blocks, scale=atlas.scale, offset=atlas.offset)
+    return atlas
 
 
 def cpu_model() -> str:
@@ -317,7 +345,7 @@ def _is_split_kernel(name: str) -> bool:
     return len(args) >= 4 and args[3] == "false"
 
 
-def summarize_counters(dirs, kernels=("astc_attn_kernel", "fp16_attn_kernel")) -> str:
+def summarize_counters(dirs, kernels=("astc_attn_kernel", "fp16_attn_kernel", "paged_attn_kernel")) -> str:
     """Markdown table of every PMC counter found under `dirs` (rocprofv3
     --pmc output), mean per dispatch, for the kernels whose names start with
     one of `kernels`."""
@@ -430,29 +458,50 @@ def cpu_leg_ragged(q, kv, seconds, sample_bytes, what):
             "sample_bytes": int(sample_bytes)}
 
 
-def main_ragged(a, torch, gpu):
-    """A ragged batch in page pools with block tables (akv_hip_paged_decode_attention)."""
-    from astc_kv.atlas import block_class_histogram
-    from astc_kv.paged import build_paged
-    from oracle import attention_ref as R
-    from oracle.paged_ref import host_kv
-
+def ragged_inputs(a):
+    """The ragged batch's sequence lengths, paged pool and queries (seeded;
+    from the --cache directory when a previous run saved them)."""
+    from astc_kv.paged import PagedKV, build_paged
     bx, by = (int(x) for x in a.block.split("x"))
     rng = np.random.default_rng(20261202)
     lens = rng.integers(a.min_tokens, a.tokens + 1, size=a.ragged).tolist()
     log(f"building {a.ragged} paged sequences, {sum(lens)} tokens: {ragged_workload_name(a)}")
     t0 = time.perf_counter()
-    k, v = [], []
-    for t in lens:
-        kk = rng.normal(size=(a.kv_heads, t, a.dim)).astype(np.float32)
-        kk[..., :4] *= 8.0
-        k.append(kk.astype(np.float16))
-        v.append(rng.normal(0.0, 0.5, size=(a.kv_heads, t, a.dim)).astype(np.float32))
-    pk = build_paged(k, v, a.layout, (bx, by), a.page, a.quality, a.k_format, a.tail, seed=7,
-                     progress=lambda i, n: log(f"  encoded {i}/{n} sequences") if i % 8 == 0 or i == n else None)
-    setup_s = time.perf_counter() - t0
+    path = _cache_path(a, f"paged-q{a.quality:g}")
+    if path is not None and path.exists():
+        z = np.load(path)
+        pk = PagedKV(z["k_pages"], z["k_meta"] if "k_meta" in z else None, z["v_blocks"], z["v_scale"], z["v_offset"],
+                     z["block_table"], z["seq_lens"], z["v_tail"] if "v_tail" in z else None, a.dim, a.layout, bx, by,
+                     a.page, a.k_format)
+        q = z["q"]
+    else:
+        k, v = [], []
+        for t in lens:
+            kk = rng.normal(size=(a.kv_heads, t, a.dim)).astype(np.float32)
+            kk[..., :4] *= 8.0
+            k.append(kk.astype(np.float16))
+            v.append(rng.normal(0.0, 0.5, size=(a.kv_heads, t, a.dim)).astype(np.float32))
+        pk = build_paged(k, v, a.layout, (bx, by), a.page, a.quality, a.k_format, a.tail, seed=7,
+                         progress=lambda i, n: log(f"  encoded {i}/{n} sequences") if i % 8 == 0 or i == n else None)
+        del k, v
+        q = rng.normal(size=(a.ragged, a.query_heads, a.dim)).astype(np.float32)
+        if path is not None:
+            path.parent.mkdir(parents=True, exist_ok=True)
+            np.savez(path, q=q, **{f: getattr(pk, f) for f in ("k_pages", "k_meta", "v_blocks", "v_scale",
+                                                               "v_offset", "block_table", "seq_lens", "v_tail")
+                                   if getattr(pk, f) is not None})
+    return lens, pk, q, time.perf_counter() - t0
+
+
+def main_ragged(a, torch, gpu):
+    """A ragged batch in page pools with block tables (akv_hip_paged_decode_attention)."""
+    from astc_kv.atlas import block_class_histogram
+    from oracle import attention_ref as R
+    from oracle.paged_ref import host_kv
+
+    bx, by = (int(x) for x in a.block.split("x"))
+    lens, pk, q, setup_s = ragged_inputs(a)
     cache = gpu.DevicePagedKV.from_host(pk)
-    q = rng.normal(size=(a.ragged, a.query_heads, a.dim)).astype(np.float32)
     qt = torch.from_numpy(q).cuda()
     params = gpu.paged_params(cache, a.query_heads, a.tile or None)
     s = params.splits
@@ -568,7 +617,7 @@ def time_atlas(a, torch, gpu, qt, kt, dev, params, steps, warmup):
     def resident(i):
         gpu.decode_attention(qt, kt, dev, params=params, partial=partial, stats=stats, out=out)
 
-    ms_resident, _ = time_graph(torch, resident, steps, warmup, not a.no_graph)
+    ms_resident = float("nan") if a.no_resident else time_graph(torch, resident, steps, warmup, not a.no_graph)[0]
     del pool
     return ms_step, ms_resident, pool_n, mode
 
@@ -706,7 +755,7 @@ def main(argv=None):
         return main_fixture(a, torch, gpu)
     if a.ragged:
         return main_ragged(a, torch, gpu)
-    from astc_kv.atlas import block_class_histogram, build_atlas
+    from astc_kv.atlas import block_class_histogram
     from oracle import astc_oracle as O
     from oracle import attention_ref as R
 
@@ -714,12 +763,12 @@ def main(argv=None):
     log(f"encoding the V atlas: {workload_name(a)}")
     t_setup = time.perf_counter()
     q, k, v = make_inputs(a)
-    atlas = build_atlas(v, a.layout, (bx, by), a.page, a.quality)
+    atlas = cached_atlas(a, v, a.quality)
     setup_s = time.perf_counter() - t_setup
     atlas_cmp = None
     if a.compare_quality > 0 and a.compare_quality != a.quality:
         log(f"encoding the comparison atlas at quality {a.compare_quality:g}")
-        atlas_cmp = build_atlas(v, a.layout, (bx, by), a.page, a.compare_quality)
+        atlas_cmp = cached_atlas(a, v, a.compare_quality)
     del v
     dev = gpu.DeviceAtlas.from_host(atlas)
     qt = torch.from_numpy(q).cuda()
@@ -824,8 +873,8 @@ def main(argv=None):
         "cpu_baseline": cpu,
         "v_blocks": block_class_histogram(atlas.blocks, bx, by, a.layout),
         "quality_50" if a.compare_quality == 50 else "quality_compare": cmp,
-        "resident_single_set": {"us_per_step": round(ms_resident * 1e3, 3),
-                                "GB/s": round(nbytes["step"] / (ms_resident * 1e-3) / 1e9, 2)},
+        "resident_single_set": None if a.no_resident else {
+            "us_per_step": round(ms_resident * 1e3, 3), "GB/s": round(nbytes["step"] / (ms_resident * 1e-3) / 1e9, 2)},
         "fp16_control": {"us_per_step": round(ms_fp16 * 1e3, 3), "bytes_per_step": fp16_bytes,
                          "GB/s": round(fp16_bytes / (ms_fp16 * 1e-3) / 1e9, 2), "tile_tokens": fparams.tile_tokens,
                          "astc_speedup": round(ms_fp16 / ms_step, 4)},
