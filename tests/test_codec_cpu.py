@@ -315,3 +315,29 @@ def test_block_classes_against_oracle_kinds_and_spec_fields(bx, by):
     assert h["blocks"] == len(blocks)
     assert abs(h["table_path"] + h["compute_path"] + h["void_extent"] + h["error"] - 1) < 1e-3
     assert abs(sum(h["partitions"].values()) - np.mean(kinds == 0)) < 1e-3
+
+
+@pytest.mark.parametrize("pair", [("records", 17), ("science", 5)])
+def test_encoder_quality_against_astcenc_record(golden, pair):
+    """Own encoder at quality 98 on the reference's captured, normalised V
+    (fixed_input.npz of scripts/probe_block_geometry.py:142-155): the error
+    tests/golden/encoder_quality.py recorded is reproduced, and stays within
+    1.35x of astcenc 5.7.0's recorded quality-98 error on the same image."""
+    import json
+    cap, layer = pair
+    rec = next(r for r in json.loads((golden / "encoder_quality.json").read_text())["pairs"]
+               if r["capture"] == cap and r["layer"] == layer)
+    z = np.load(golden / "geometry" / f"{cap}_l{layer}_fixed_input.npz")
+    scalar = z["normalized_padded"].astype(np.float32)
+    enc = codec.AstcEncoder((6, 6), 98)
+    try:
+        dec = []
+        for img in scalar:
+            image = np.ones(img.shape + (4,), np.float32)
+            image[..., :3] = img[..., None]
+            dec.append(enc.roundtrip(image)[1][..., 0])
+    finally:
+        enc.close()
+    err = float(np.sum(np.square(np.stack(dec).astype(np.float64) - scalar)))
+    assert err == pytest.approx(rec["this_q98"]["normalized_padded_error_sse"], rel=1e-9)
+    assert err <= 1.35 * rec["astcenc_q98"]["normalized_padded_error_sse"]
