@@ -62,11 +62,20 @@ constexpr int kInfoRangeShift = 14;             // bits 14-17: weight range
 constexpr int kInfoLevelsShift = 18;            // bits 18-23: table row length (weight levels)
 constexpr uint32_t kInfoIdentity = 1u << 24;
 constexpr uint32_t kInfoTable = 1u << 25;
-// A reduced weight grid with one plane, whose texel weights a fill stage
-// (fill_weights) infills once per chunk: texel i's weight (0..64) is byte i
-// from dword (bits 27-31) of the record on, just past the endpoint pairs.
+// A reduced weight grid with one plane whose texels a fill stage
+// (fill_values) computes once per chunk: texel i is entry slot * ntex + i of
+// the chunk's fill area (FillArea), slot in bits 27-31.
 constexpr uint32_t kInfoFilled = 1u << 26;
 constexpr int kInfoFillShift = 27;
+constexpr int kFillSlots = 32;
+
+// Texel values of the chunk's filled blocks: 1024 RGBA texels (8 bytes
+// each, 8 KB: 32 blocks of 6x5) or 2048 scalar texels (2 bytes, 4 KB).
+template <int NCH>
+struct FillArea {
+    static constexpr int kTexels = NCH == 4 ? 1024 : 2048;
+    uint16_t v[kTexels * NCH];
+};
 
 template <int NCH>
 struct BlockDesc {
@@ -648,10 +657,9 @@ __device__ inline uint4 block_part_words(uint4 raw, uint4 words) {
 // `cv` is this lane's scratch for the unquantised colour values
 // (kColourScratchWords dwords, four values per dword).
 // Every table read is from LDS.
-// With FILL, a reduced single-plane grid whose `ntex` texel weights fit
-// after its endpoint pairs in the endpoint/table union and the weight fields
-// (84 bytes) is marked kInfoFilled: the caller then runs fill_weights on it
-// before the texel stage.
+// With FILL, a reduced single-plane grid of a footprint of at most 64
+// texels is marked kInfoFilled: the caller gives it a slot of its fill area
+// (or clears the mark) and runs fill_values before the texel stage.
 template <int NCH, bool CAP = false, bool FILL = false>
 __device__ __attribute__((always_inline)) inline void decode_header(const LdsTables& L, BlockDesc<NCH>& d,
                                                                    uint32_t* cv, int ntex = 0) {
@@ -771,12 +779,11 @@ __device__ __attribute__((always_inline)) inline void decode_header(const LdsTab
             for (int ch = 0; ch < NCH; ++ch) d.ep[p][ch] = ep[ch];
         }
     }
-    const int woff = parts * NCH;   // dwords of endpoint pairs
-    const bool fill = FILL && !identity && !dual && 4 * woff + ntex <= 84;
+    const bool fill = FILL && !identity && !dual && ntex <= 64;
     d.info = (md & 0xFFu) | (dual ? kInfoDual : 0u) | (ccs << 9) | (uint32_t(nb) << kInfoNbShift) |
              (uint32_t(wrange) << kInfoRangeShift) | (uint32_t(levels) << kInfoLevelsShift) |
              (identity ? kInfoIdentity : 0u) | (table ? kInfoTable : 0u) |
-             (fill ? kInfoFilled | (uint32_t(woff) << kInfoFillShift) : 0u);
+             (fill ? kInfoFilled : 0u);
 }
 
 // Weight field `idx` (grid order, planes interleaved) of a block.
@@ -841,17 +848,15 @@ __device__ inline uint2 texel_identity(const BlockDesc<NCH>& d, const LdsTables&
     else return uint2{pack_fp16_rtz(C[0], kCBias) & 0xFFFFu, 0u};
 }
 
-// Stage 1b: the texel weights of the kInfoFilled blocks `list[0..n)`, by
-// whole waves, one lane per texel: a wave takes 64 / span blocks per pass
-// (span: the texel count rounded up to 16, 32 or 64, so ntex <= 64). Each
-// lane writes its texel's weight byte over the block's endpoint/table union
-// and weight fields, which the other lanes of the same block read: the
-// block's lanes are one wave's, and a lane's store depends on its own loads,
-// so the wave's loads have all returned when its first store issues. A
-// workgroup barrier must follow before the texel stage.
+// Stage 1b: the texels of the kInfoFilled blocks `list[0..n)` (block
+// list[e] has slot e), by whole waves, one lane per texel: a wave takes
+// 64 / span blocks per pass (span: the texel count rounded up to 16, 32 or
+// 64, so ntex <= 64). Each lane infills its texel's weight, finds its
+// partition and interpolates the endpoints, into `fa`. A workgroup barrier
+// must follow before the texel stage.
 template <int NCH, int NT>
-__device__ inline void fill_weights(BlockDesc<NCH>* desc, const LdsTables& L, Footprint f, const uint8_t* list, int n,
-                                    int tid) {
+__device__ inline void fill_values(const BlockDesc<NCH>* desc, const LdsTables& L, Footprint f, const uint8_t* list,
+                                   int n, FillArea<NCH>& fa, int tid) {
     const int span = f.ntex <= 16 ? 16 : f.ntex <= 32 ? 32 : 64;
     const int per = 64 / span;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -861,23 +866,28 @@ __device__ inline void fill_weights(BlockDesc<NCH>* desc, const LdsTables& L, Fo
     for (int base = wave * per; base < n; base += (NT / 64) * per) {
         const int e = base + sub;
         if (e < n && t < f.ntex) {
-            BlockDesc<NCH>& d = desc[list[e]];
+            const BlockDesc<NCH>& d = desc[list[e]];
             const uint32_t info = d.info;
-            const int w = texel_weight(d, L, f.bx, f.ds, f.dt, info, x, y, 0);
-            reinterpret_cast<uint8_t*>(d.tab)[4 * int(info >> kInfoFillShift) + t] = uint8_t(w);
+            const uint32_t wp = weight_pair(texel_weight(d, L, f.bx, f.ds, f.dt, info, x, y, 0));
+            const int p = int(__builtin_amdgcn_ubfe(d.part[t >> 4], uint32_t(2 * t), 2));
+            uint32_t C[NCH];
+#pragma unroll
+            for (int ch = 0; ch < NCH; ++ch) C[ch] = interp_c(d.ep[p][ch], wp);
+            const int slot = e * f.ntex + t;
+            if constexpr (NCH == 4)
+                *reinterpret_cast<uint2*>(&fa.v[4 * slot]) = uint2{pack_fp16_rtz(C[0], C[1]), pack_fp16_rtz(C[2], C[3])};
+            else
+                fa.v[slot] = uint16_t(pack_fp16_rtz(C[0], kCBias));
         }
     }
 }
 
-// Stage 2 of a kInfoFilled block: the weight byte, then the interpolation.
+// Stage 2 of a kInfoFilled block: its texel from the fill area.
 template <int NCH>
-__device__ inline uint2 texel_filled(const BlockDesc<NCH>& d, uint32_t info, int i, int p) {
-    const uint32_t wp = weight_pair(int(reinterpret_cast<const uint8_t*>(d.tab)[4 * int(info >> kInfoFillShift) + i]));
-    uint32_t C[NCH];
-#pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) C[ch] = interp_c(d.ep[p][ch], wp);
-    if constexpr (NCH == 4) return uint2{pack_fp16_rtz(C[0], C[1]), pack_fp16_rtz(C[2], C[3])};
-    else return uint2{pack_fp16_rtz(C[0], kCBias) & 0xFFFFu, 0u};
+__device__ inline uint2 texel_filled(const FillArea<NCH>& fa, uint32_t info, int i, int ntex) {
+    const int slot = int(info >> kInfoFillShift) * ntex + i;
+    if constexpr (NCH == 4) return *reinterpret_cast<const uint2*>(&fa.v[4 * slot]);
+    else return uint2{uint32_t(fa.v[slot]), 0u};
 }
 
 // Stage 2: the FP16 values of texel (x, y) of a block (NCH == 4:
@@ -901,11 +911,11 @@ __device__ inline uint2 texel_fp16(const BlockDesc<NCH>& d, const LdsTables& L, 
 // together), and the compute path runs only where a block needs it. The
 // table read of a block that is not a table may land anywhere in the first
 // kilobyte past its record (entry < 128); its value is replaced.
-// FILL: the kernel runs the fill stage (kInfoFilled blocks are filled).
+// FILL: the kernel runs the fill stage (kInfoFilled blocks are in `fa`).
 template <int NCH, int K, bool FILL>
 __device__ inline void texels_fp16(const BlockDesc<NCH>* desc, const int (&blk)[K], const int (&i)[K],
                                    const int (&x)[K], const int (&y)[K], const LdsTables& L, Footprint f,
-                                   uint2 (&out)[K]) {
+                                   const FillArea<NCH>* fa, uint2 (&out)[K]) {
     uint32_t info[K];
     int p[K];
     bool all_table = true;
@@ -929,7 +939,7 @@ __device__ inline void texels_fp16(const BlockDesc<NCH>* desc, const int (&blk)[
         for (int k = 0; k < K; ++k)
             if (!(info[k] & kInfoTable)) {
                 if (FILL && (info[k] & kInfoFilled))
-                    out[k] = texel_filled<NCH>(desc[blk[k]], info[k], i[k], p[k]);
+                    out[k] = texel_filled<NCH>(*fa, info[k], i[k], f.ntex);
                 else if (NCH == 4 && (info[k] & (kInfoIdentity | kInfoDual)) == kInfoIdentity)
                     out[k] = texel_identity<NCH>(desc[blk[k]], L, info[k], i[k], p[k]);
                 else

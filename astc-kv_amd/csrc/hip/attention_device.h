@@ -543,7 +543,9 @@ __device__ inline void combine_waves(float* comb, WaveStats& ws, AttnState<D>& s
 
 // --- ASTC split kernel -------------------------------------------------------
 
-template <int D, int NCH, bool WIDE = false>
+// FILLS: room for the fill stage's texels (the split kernel's; the paged
+// kernel has no fill stage).
+template <int D, int NCH, bool WIDE = false, bool FILLS = true>
 struct AstcShared {
     using C = Cfg<D, NCH, WIDE>;
     LdsTables tabs;
@@ -551,7 +553,8 @@ struct AstcShared {
         struct {
             BlockDesc<NCH> desc[C::kMaxBlocks];
             uint32_t cv[C::kMaxBlocks][kColourScratchWords];   // header-stage colour values, per lane
-            uint8_t fill[C::kMaxBlocks];                       // blocks for the fill stage (kInfoFilled)
+            uint8_t fill[kFillSlots];                          // blocks for the fill stage (kInfoFilled)
+            FillArea<NCH> fv[FILLS ? 1 : 0];                   // their texels
         } h;
         float comb[kWaves * D * kMaxG];      // final per-wave accumulators
     } u;
@@ -589,7 +592,8 @@ __device__ inline void tile_rows(const uint32_t* tokrow, int t0, int g, uint32_t
 template <int NCH, bool FILL>
 __device__ __attribute__((always_inline)) inline void column_texels(const BlockDesc<NCH>* desc, const LdsTables& L,
                                                                     Footprint f, const uint32_t (&rows)[4], int bcol,
-                                                                    int xin, uint2 (&tv)[4]) {
+                                                                    int xin, const FillArea<NCH>* fa,
+                                                                    uint2 (&tv)[4]) {
     int bk[4], ik[4], xk[4], yk[4];
 #pragma unroll
     for (int tk = 0; tk < 4; ++tk) {
@@ -598,7 +602,7 @@ __device__ __attribute__((always_inline)) inline void column_texels(const BlockD
         xk[tk] = xin;
         yk[tk] = int(rows[tk] & 0xFF);
     }
-    texels_fp16<NCH, 4, FILL>(desc, bk, ik, xk, yk, L, f, tv);
+    texels_fp16<NCH, 4, FILL>(desc, bk, ik, xk, yk, L, f, fa, tv);
 }
 
 // Row table of a chunk: token t -> (first block of its block row) << 16 |

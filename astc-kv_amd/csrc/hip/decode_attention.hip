@@ -87,6 +87,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
         if (wave == 0) qst.store(a.qscale, &sh.q[0][0]);
     if (tid < kPathKeys) sh.key_count[tid] = 0;
     if (tid == 0) sh.nfill = 0;
+    // Blocks the fill area holds (kFillSlots at most).
+    const int fill_slots = min(kFillSlots, FillArea<NCH>::kTexels / f.ntex);
 
     // This lane's texel columns: x = n16 + 16 * kc -> block column | x in
     // block << 16 (one register each).
@@ -182,13 +184,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
         if (tid < nblk) {
             const int bi = sh.order[tid];
             decode_header<NCH, D == 128, true>(sh.tabs, sh.u.h.desc[bi], sh.u.h.cv[tid], f.ntex);
-            if (sh.u.h.desc[bi].info & kInfoFilled) sh.u.h.fill[atomicAdd(&sh.nfill, 1u)] = uint8_t(bi);
+            if (sh.u.h.desc[bi].info & kInfoFilled) {   // a slot of the fill area, or the compute path
+                const uint32_t slot = atomicAdd(&sh.nfill, 1u);
+                if (slot < uint32_t(fill_slots)) {
+                    sh.u.h.fill[slot] = uint8_t(bi);
+                    sh.u.h.desc[bi].info |= slot << kInfoFillShift;
+                } else {
+                    sh.u.h.desc[bi].info &= ~kInfoFilled;
+                }
+            }
         }
         __syncthreads();
-        // 2b. Reduced weight grids: every texel weight infilled once, by whole
-        // waves, rather than at each texel lookup.
+        // 2b. Reduced weight grids: every texel of those blocks computed once,
+        // by whole waves, rather than at each texel lookup.
         if (const int nfill = __builtin_amdgcn_readfirstlane(int(sh.nfill))) {
-            fill_weights<NCH, kThreads>(sh.u.h.desc, sh.tabs, f, sh.u.h.fill, nfill, tid);
+            fill_values<NCH, kThreads>(sh.u.h.desc, sh.tabs, f, sh.u.h.fill, min(nfill, fill_slots), sh.u.h.fv[0], tid);
             __syncthreads();
             if (tid == 0) sh.nfill = 0;   // read by every thread before the barrier above
         }
@@ -204,7 +214,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
 #pragma unroll
                 for (int kc = 0; kc < C::kColGroups; ++kc) {
                     uint2 tv[4];
-                    column_texels<NCH, true>(sh.u.h.desc, sh.tabs, f, rows, colpk[kc] & 0xFFFF, colpk[kc] >> 16, tv);
+                    column_texels<NCH, true>(sh.u.h.desc, sh.tabs, f, rows, colpk[kc] & 0xFFFF, colpk[kc] >> 16, sh.u.h.fv, tv);
                     const int x = n16 + 16 * kc;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -232,7 +242,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
                             tile_rows(sh.tokrow, tb0 + 16 * t, g, rows);
                         }
                         uint2 tv[4];
-                        column_texels<NCH, true>(sh.u.h.desc, sh.tabs, f, rows, colpk[kc] & 0xFFFF, colpk[kc] >> 16, tv);
+                        column_texels<NCH, true>(sh.u.h.desc, sh.tabs, f, rows, colpk[kc] & 0xFFFF, colpk[kc] >> 16, sh.u.h.fv, tv);
                         texel_operands<NCH>(tv, va);
                     });
             }

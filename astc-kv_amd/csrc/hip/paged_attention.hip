@@ -43,7 +43,7 @@ struct PagedArgs {
 
 template <int D, int NCH>
 struct PagedShared {
-    AstcShared<D, NCH> a;
+    AstcShared<D, NCH, false, false> a;
     int32_t pages[kMaxSplitPages];     // the split's pages, from its first
 };
 
@@ -74,7 +74,7 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
     // dwords and D/32 (offset, scale) dwords.
     constexpr int kKWords = KU4 ? D / 16 : 4 * (D / 32);
     __shared__ PagedShared<D, NCH> shp;
-    AstcShared<D, NCH>& sh = shp.a;
+    AstcShared<D, NCH, false, false>& sh = shp.a;
     const AkvPagedParams& p = a.p;
     const Footprint f = a.fp;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -290,7 +290,7 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
                 }
                 uint2 tv[4];
                 if (in_tail) tail_texels<D, NCH>(tail, trow, n16 + 16 * kc, tv);
-                else column_texels<NCH, false>(sh.u.h.desc, sh.tabs, f, rows, colpk[kc] & 0xFFFF, colpk[kc] >> 16, tv);
+                else column_texels<NCH, false>(sh.u.h.desc, sh.tabs, f, rows, colpk[kc] & 0xFFFF, colpk[kc] >> 16, nullptr, tv);
                 texel_operands<NCH>(tv, va);
             };
             if constexpr (KU4)
