@@ -140,22 +140,29 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
         // 2. Block headers, with the chunk's blocks sorted by decode-path class
         // so that the lanes of a wave take the same branches. Each block's raw
         // bits wait in its own descriptor slot; the lane that decodes a block
-        // reads them from there and overwrites that slot.
+        // reads them from there and overwrites that slot. A chunk of one
+        // wave's blocks gains nothing from the sort: each lane decodes the
+        // block it stashed, with no barrier.
+        const bool sorted = nblk > 64;
         int key = 0, rank = 0;
         if (tid < nblk) {
-            key = block_path_key(raw_now);
             stash_block(sh.u.h.desc[tid], raw_now);
-            rank = int(atomicAdd(&sh.key_count[key], 1u));
+            if (sorted) {
+                key = block_path_key(raw_now);
+                rank = int(atomicAdd(&sh.key_count[key], 1u));
+            }
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
             if (tid + i * kThreads < C::kMaxTok)
                 sh.tokrow[tid + i * kThreads] = token_row_entry(tid + i * kThreads, ntok, a.mag_by, f, cols, c0 % by);
-        __syncthreads();   // class counts complete
-        static_assert(kPathKeys == 64, "one class per lane");
-        place_by_class(sh.key_count, sh.order, key, rank, tid < nblk, tid);
-        __syncthreads();   // sorted order complete (and every count read)
-        if (wave == 0) sh.key_count[lane] = 0;   // for the next chunk (two barriers away)
+        if (sorted) {
+            __syncthreads();   // class counts complete
+            static_assert(kPathKeys == 64, "one class per lane");
+            place_by_class(sh.key_count, sh.order, key, rank, tid < nblk, tid);
+            __syncthreads();   // sorted order complete (and every count read)
+            if (wave == 0) sh.key_count[lane] = 0;   // for the next chunk (two barriers away)
+        }
         if constexpr (!DUMP) {
 #pragma unroll
             for (int t = kKEarly; t < TPG; ++t)
@@ -182,7 +189,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
             }
         }
         if (tid < nblk) {
-            const int bi = sh.order[tid];
+            const int bi = sorted ? int(sh.order[tid]) : tid;
             decode_header<NCH, D == 128, true>(sh.tabs, sh.u.h.desc[bi], sh.u.h.cv[tid], f.ntex);
             if (sh.u.h.desc[bi].info & kInfoFilled) {   // a slot of the fill area, or the compute path
                 const uint32_t slot = atomicAdd(&sh.nfill, 1u);
