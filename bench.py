@@ -613,13 +613,16 @@ def time_atlas(a, torch, gpu, qt, kt, dev, params, steps, warmup):
 
     torch.cuda.synchronize()
     ms_step, mode = time_graph(torch, step, steps, warmup, not a.no_graph)
+    # The same launches one by one (what a profiler's per-kernel average sees:
+    # without graph replay consecutive launches do not overlap).
+    ms_eager = time_graph(torch, step, steps, warmup, False)[0] if mode == "hipgraph" else ms_step
 
     def resident(i):
         gpu.decode_attention(qt, kt, dev, params=params, partial=partial, stats=stats, out=out)
 
     ms_resident = float("nan") if a.no_resident else time_graph(torch, resident, steps, warmup, not a.no_graph)[0]
     del pool
-    return ms_step, ms_resident, pool_n, mode
+    return ms_step, ms_resident, pool_n, mode, ms_eager
 
 
 def cpu_leg(q, k, v_rest, seconds, step_bytes_, what):
@@ -685,7 +688,7 @@ def main_fixture(a, torch, gpu):
         if tile is None and name == "reference_tile":
             continue
         p = gpu.make_params(dev, a.query_heads, tile)
-        ms, ms_res, pool_n, mode = time_atlas(a, torch, gpu, qt, kt, dev, p, a.steps, a.warmup)
+        ms, ms_res, pool_n, mode, _ = time_atlas(a, torch, gpu, qt, kt, dev, p, a.steps, a.warmup)
         runs[name] = {"tile_tokens": p.tile_tokens, "splits": p.splits, "us_per_step": round(ms * 1e3, 3),
                       "us_per_step_resident": round(ms_res * 1e3, 3), "pool_sets": pool_n,
                       "GB/s": round(nbytes["step"] / (ms * 1e-3) / 1e9, 2)}
@@ -781,13 +784,13 @@ def main(argv=None):
         copy_calibration(torch, a.copy_calibration_mb)
 
     log(f"timing {a.steps} steps (tile {params.tile_tokens}, {params.splits} splits)")
-    ms_step, ms_resident, pool_n, mode = time_atlas(a, torch, gpu, qt, kt, dev, params, a.steps, a.warmup)
+    ms_step, ms_resident, pool_n, mode, ms_eager = time_atlas(a, torch, gpu, qt, kt, dev, params, a.steps, a.warmup)
 
     cmp = None
     if atlas_cmp is not None:
         log(f"timing the quality {a.compare_quality:g} atlas")
         dev_c = gpu.DeviceAtlas.from_host(atlas_cmp)
-        ms_c, ms_c_res, _, _ = time_atlas(a, torch, gpu, qt, kt, dev_c, params, a.steps, a.warmup)
+        ms_c, ms_c_res, _, _, _ = time_atlas(a, torch, gpu, qt, kt, dev_c, params, a.steps, a.warmup)
         cmp = {"quality": a.compare_quality, "us_per_step": round(ms_c * 1e3, 3),
                "us_per_step_resident": round(ms_c_res * 1e3, 3),
                "GB/s": round(nbytes["step"] / (ms_c * 1e-3) / 1e9, 2),
@@ -869,7 +872,8 @@ def main(argv=None):
                      "traffic": traffic["bytes"] if traffic else None,
                      "traffic_source": traffic["source"] if traffic else None,
                      "kernel": "astc_attn_kernel (split + in-kernel merge, ASTC V)",
-                     "bytes_per_launch": nbytes["step"], "us_per_launch": round(ms_step * 1e3, 3)},
+                     "bytes_per_launch": nbytes["step"], "us_per_launch": round(ms_step * 1e3, 3),
+                     "eager_us_per_launch": round(ms_eager * 1e3, 3)},
         "cpu_baseline": cpu,
         "v_blocks": block_class_histogram(atlas.blocks, bx, by, a.layout),
         "quality_50" if a.compare_quality == 50 else "quality_compare": cmp,
