@@ -226,25 +226,27 @@ constexpr int ise_max_values(int r, int cap, int budget) {
 // up are skipped, at two branch points (past 16 and past 36 values), so that
 // the groups below stay straight-line code. A vlim the compiler knows to be
 // >= the value count removes the branches.
-template <int GS, int NG, typename Group>
+// B1, B2: the two branch points (value counts), 16 and 36 for weight
+// sequences, 4 and 8 for colour sequences.
+template <int GS, int NG, int B1 = 16, int B2 = 36, typename Group>
 __device__ __attribute__((always_inline)) inline void ise_groups(int vlim, Group&& group) {
-    constexpr int G16 = NG < (16 + GS - 1) / GS ? NG : (16 + GS - 1) / GS;
-    constexpr int G36 = NG < (36 + GS - 1) / GS ? NG : (36 + GS - 1) / GS;
-    static_for<0, G16>(group);
-    if (vlim > 16) {
-        static_for<G16, G36>(group);
-        if (vlim > 36) static_for<G36, NG>(group);
+    constexpr int G1 = NG < (B1 + GS - 1) / GS ? NG : (B1 + GS - 1) / GS;
+    constexpr int G2 = NG < (B2 + GS - 1) / GS ? NG : (B2 + GS - 1) / GS;
+    static_for<0, G1>(group);
+    if (vlim > B1) {
+        static_for<G1, G2>(group);
+        if (vlim > B2) static_for<G2, NG>(group);
     }
 }
 
-template <int R, int V, typename Emit>
+template <int R, int V, int B1 = 16, int B2 = 36, typename Emit>
 __device__ __attribute__((always_inline)) inline void ise_unpack(const uint32_t (&s)[4], const LdsTables& L, int vlim,
                                                                  Emit&& emit) {
     constexpr akv::IseRange e = akv::kIse[R];
     constexpr int n = e.bits;
     if constexpr (e.trit) {
         constexpr int gb = 5 * n + 8;
-        ise_groups<5, (V + 4) / 5>(vlim, [&](auto gi) {
+        ise_groups<5, (V + 4) / 5, B1, B2>(vlim, [&](auto gi) {
             constexpr int p = decltype(gi)::value * gb;
             uint32_t T;
             if constexpr (n == 0) {
@@ -263,7 +265,7 @@ __device__ __attribute__((always_inline)) inline void ise_unpack(const uint32_t 
         });
     } else if constexpr (e.quint) {
         constexpr int gb = 3 * n + 7;
-        ise_groups<3, (V + 2) / 3>(vlim, [&](auto gi) {
+        ise_groups<3, (V + 2) / 3, B1, B2>(vlim, [&](auto gi) {
             constexpr int p = decltype(gi)::value * gb;
             uint32_t Q;
             if constexpr (n == 0) {
@@ -280,7 +282,7 @@ __device__ __attribute__((always_inline)) inline void ise_unpack(const uint32_t 
             });
         });
     } else {
-        static_for<0, V>([&](auto ji) { emit(ji, bits_at<decltype(ji)::value * n, n>(s)); });
+        ise_groups<1, V, B1, B2>(vlim, [&](auto ji) { emit(ji, bits_at<decltype(ji)::value * n, n>(s)); });
     }
 }
 
@@ -288,12 +290,14 @@ __device__ __attribute__((always_inline)) inline void ise_unpack(const uint32_t 
 // 111 bits after the 17-bit header.
 // The values are packed four to a dword (value j in byte j % 4 of dword
 // j / 4) and stored as dwords: ColourScratch.
-template <int R>
+// vlim (wave-uniform): with CAP, the values from vlim on (past 4 or 8) are
+// not decoded (their bytes of cv stay zero; the block does not read them).
+template <int R, bool CAP = false>
 __device__ __attribute__((always_inline)) inline void colour_values(const uint32_t (&s)[4], const LdsTables& L,
-                                                                    uint32_t* cv) {
+                                                                    uint32_t* cv, int vlim = 64) {
     constexpr int V = ise_max_values(R, 18, 111);
     uint32_t w[(V + 3) / 4] = {};
-    ise_unpack<R, V>(s, L, 64, [&](auto ji, uint32_t v) {
+    ise_unpack<R, V, 4, 8>(s, L, CAP ? vlim : 64, [&](auto ji, uint32_t v) {
         constexpr int j = decltype(ji)::value;
         w[j / 4] |= uint32_t(L.color_unq[R][v]) << (8 * (j % 4));
     });
@@ -323,6 +327,10 @@ __device__ __attribute__((always_inline)) inline void weight_fields(const uint32
 
 // Colour integer sequence of this lane's block: range `crange`, `nv` values
 // from bit `start` of the block `blk` (four words in LDS) -> cv (packed bytes).
+// With CAP, each pass decodes only up to the largest value count among its
+// lanes (4, 8 or all): one luminance partition needs 2 values where a high
+// range fits 13.
+template <bool CAP = false>
 __device__ __attribute__((always_inline)) inline void decode_colour_values(const uint32_t* blk, int start, int crange, int nv, const LdsTables& L,
                                             uint32_t* cv) {
     const uint4 b4 = uint4{blk[0], blk[1], blk[2], blk[3]};   // records are 4-byte aligned
@@ -330,10 +338,13 @@ __device__ __attribute__((always_inline)) inline void decode_colour_values(const
         const int r = __builtin_amdgcn_readfirstlane(crange);
         if (crange == r) {
             uint32_t s[4] = {b4.x, b4.y, b4.z, b4.w};
+            int vlim = 64;
+            if constexpr (CAP)   // the lanes of this pass are the active ones
+                vlim = __builtin_amdgcn_ballot_w64(nv > 8) ? 64 : __builtin_amdgcn_ballot_w64(nv > 4) ? 8 : 4;
             auto run = [&](auto ri) {
                 constexpr int R = decltype(ri)::value;
                 shift_and_cut(s, uint32_t(start), ise_seq_bits<R>(nv));
-                colour_values<R>(s, L, cv);
+                colour_values<R, CAP>(s, L, cv, vlim);
             };
             switch (r) {
                 case 4: run(Idx<4>{}); break;
@@ -660,7 +671,8 @@ __device__ inline uint4 block_part_words(uint4 raw, uint4 words) {
 // With FILL, a reduced single-plane grid of a footprint of at most 64
 // texels is marked kInfoFilled: the caller gives it a slot of its fill area
 // (or clears the mark) and runs fill_values before the texel stage.
-template <int NCH, bool CAP = false, bool FILL = false>
+// CCAP: decode_colour_values<true> (colour values up to the pass's largest count).
+template <int NCH, bool CAP = false, bool FILL = false, bool CCAP = false>
 __device__ __attribute__((always_inline)) inline void decode_header(const LdsTables& L, BlockDesc<NCH>& d,
                                                                    uint32_t* cv, int ntex = 0) {
     const uint32_t* blk = d.tab;        // block bits
@@ -723,7 +735,7 @@ __device__ __attribute__((always_inline)) inline void decode_header(const LdsTab
         return;
     }
     // Colour integer sequence -> unquantised colour bytes.
-    decode_colour_values(blk, color_start, crange, 2 * pairs, L, cv);
+    decode_colour_values<CCAP>(blk, color_start, crange, 2 * pairs, L, cv);
 
     // Weights: the integer sequence runs from bit 127 downwards, so in the
     // bit-reversed block it starts at bit 0; unpacked to nb-bit fields.

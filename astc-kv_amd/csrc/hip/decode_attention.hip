@@ -190,7 +190,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
         }
         if (tid < nblk) {
             const int bi = sorted ? int(sh.order[tid]) : tid;
-            decode_header<NCH, D == 128, true>(sh.tabs, sh.u.h.desc[bi], sh.u.h.cv[tid], f.ntex);
+            decode_header<NCH, D == 128, true, D == 128 && NCH == 1>(sh.tabs, sh.u.h.desc[bi], sh.u.h.cv[tid], f.ntex);
             if (sh.u.h.desc[bi].info & kInfoFilled) {   // a slot of the fill area, or the compute path
                 const uint32_t slot = atomicAdd(&sh.nfill, 1u);
                 if (slot < uint32_t(fill_slots)) {

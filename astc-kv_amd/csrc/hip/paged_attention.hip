@@ -261,7 +261,7 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
         }
         if (tid < nblk) {
             const int bi = sh.order[tid];
-            decode_header<NCH>(sh.tabs, sh.u.h.desc[bi], sh.u.h.cv[tid]);
+            decode_header<NCH, false, false, D == 128 && NCH == 1>(sh.tabs, sh.u.h.desc[bi], sh.u.h.cv[tid]);
         }
         __syncthreads();
         // 3. Tile groups; tiles at or past `full` read V from the FP16 tail.
