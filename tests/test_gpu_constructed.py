@@ -144,3 +144,30 @@ def test_paged_attention_over_random_v_blocks(gpu):
         ki, vi = host_kv(pk, i)
         ref = R.decode_attention(q[i:i + 1], ki[None], vi[None])[0]
         np.testing.assert_allclose(out[i], ref, rtol=RTOL, atol=ATOL, err_msg=f"sequence {i}")
+
+
+@pytest.mark.parametrize("layout,block,dim", [("scalar", (6, 6), 64), ("rgba", (6, 5), 64), ("rgba", (4, 4), 128),
+                                              ("scalar", (6, 6), 128), ("scalar", (8, 8), 64)])
+def test_fill_area_overflow(gpu, layout, block, dim):
+    """An atlas of reduced-grid, one-plane blocks only (from the constructed
+    and random blocks): every chunk has far more of them than the fill area's
+    32 slots, so the fill stage and the compute path for the blocks past the
+    last slot both run; the decode stays bit-exact against the oracle."""
+    from astc_kv import codec
+    from astc_kv.gpu import DeviceAtlas
+    bx, by = block
+    pool = np.concatenate([_constructed(bx, by), _random_blocks(bx * 7 + by + dim, 200000)])
+    lib = codec.load_codec_library()
+    cls = np.empty(len(pool), np.uint32)
+    assert lib.akv_block_classes(bx, by, pool.ctypes.data, len(pool), cls.ctypes.data) == 0
+    keep = ((cls & 3) == 0) & (((cls >> 4) & 1) == 0) & (((cls >> 5) & 1) == 0)
+    blocks = pool[keep]
+    assert len(blocks) > 2000
+    atlas = _atlas(blocks, layout, bx, by, dim, seed=dim)
+    print(f"{layout} {bx}x{by} D{dim}: {len(blocks)} reduced-grid blocks, {atlas.tokens} tokens", flush=True)
+    dev = DeviceAtlas.from_host(atlas)
+    expect = _oracle_u(atlas)
+    for tile in (None, 48):
+        got = gpu.decode_values(dev, tile).cpu().numpy().astype(np.float32)
+        bad = np.argwhere(got.view(np.uint32) != expect.view(np.uint32))
+        assert bad.size == 0, f"tile {tile}: {len(bad)} values differ, first (b, h, t, d) {bad[0].tolist()}"
