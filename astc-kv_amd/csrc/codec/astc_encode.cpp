@@ -8,13 +8,18 @@
 //   * constant blocks -> LDR void-extent block;
 //   * colour endpoint mode from the channel structure: luminance (CEM 0),
 //     luminance+alpha (CEM 4), RGB (CEM 8) or RGBA (CEM 12);
-//   * 1 partition, plus 2 and 3 partitions whose seed is chosen by matching the
-//     partition table against a k-means clustering of the texels;
+//   * 1 partition, plus 2 and 3 (4 at quality >= 90) partitions whose seeds
+//     are chosen by matching the partition table against a k-means clustering
+//     of the texels (the best 1, 2 or 4 seeds per count, more at higher
+//     quality);
 //   * weight grids: the full footprint and, at high effort, grids one or two
 //     texels smaller; every weight range whose colour data still fits;
-//   * per candidate: principal-axis line fit, least-squares endpoint refinement,
-//     then the candidate is packed and decoded exactly and scored by squared
-//     error of the decoded FP16 texels.
+//   * per candidate: principal-axis line fit, up to four rounds of
+//     least-squares endpoint refinement, then the candidate is packed and
+//     decoded exactly and scored by squared error of the decoded FP16 texels;
+//   * at quality >= 90, luminance candidates on the full grid also try the
+//     neighbouring quantised endpoint codes (3 x 3 per partition, in value
+//     order) and keep the pair of least error.
 #include <algorithm>
 #include <array>
 #include <cmath>
@@ -41,6 +46,9 @@ struct Plan {
     const AkvTables* t = nullptr;
     std::vector<GridMode> modes;          // single-plane modes, one per (grid, range)
     uint8_t nearest_color[kNumRanges][256];
+    // The codes of the next lower and next higher colour value of a range
+    // (the code itself at either end).
+    uint8_t color_down[kNumRanges][256], color_up[kNumRanges][256];
     uint8_t nearest_weight[12][65];
     uint16_t trit_code[243];
     uint8_t quint_code[125];
@@ -86,6 +94,17 @@ const Plan& plan_for(const AkvTables& t) {
                 if (d < bestd) { bestd = d; best = v; }
             }
             p->nearest_color[r][target] = uint8_t(best);
+        }
+        for (int v = 0; v < levels; ++v) {
+            const int u = t.color_unq[r][v];
+            int dn = v, up = v, dnu = -1, upu = 256;
+            for (int c = 0; c < levels; ++c) {
+                const int cu = t.color_unq[r][c];
+                if (cu < u && cu > dnu) { dnu = cu; dn = c; }
+                if (cu > u && cu < upu) { upu = cu; up = c; }
+            }
+            p->color_down[r][v] = uint8_t(dn);
+            p->color_up[r][v] = uint8_t(up);
         }
     }
     for (int r = 0; r < 12; ++r) {
@@ -309,7 +328,7 @@ struct PartitionLayout {
 
 // Build one packed candidate for a partition layout, grid mode and effort.
 void make_candidate(const Plan& plan, const BlockInput& in, const PartitionLayout& pl, const GridMode& gm,
-                    int refine, Candidate& best) {
+                    int refine, Candidate& best, bool polish = false) {
     const AkvTables& t = *plan.t;
     const int pc = pl.count, cem = in.cem;
     const int pairs = pc * ((cem >> 2) + 1);
@@ -392,6 +411,40 @@ void make_candidate(const Plan& plan, const BlockInput& in, const PartitionLayou
             for (int k = 0; k < C; ++k) {
                 lo[p][k] = float(std::clamp((r0[k] * s11 - r1[k] * s01) / det, 0.0, 1.0));
                 hi[p][k] = float(std::clamp((r1[k] * s00 - r0[k] * s01) / det, 0.0, 1.0));
+            }
+        }
+    }
+    // Luminance, identity grid, highest effort: per partition, the quantised
+    // endpoint pair and its neighbours one colour level down or up (nine
+    // pairs), each with its texels' nearest weights; the pair of least
+    // squared error (8-bit endpoint domain) stays.
+    if (polish && C == 1 && gm.identity) {
+        for (int p = 0; p < pc; ++p) {
+            const int lo_c[3] = {qlo[p][0], plan.color_down[crange][qlo[p][0]], plan.color_up[crange][qlo[p][0]]};
+            const int hi_c[3] = {qhi[p][0], plan.color_down[crange][qhi[p][0]], plan.color_up[crange][qhi[p][0]]};
+            double best_e = 1e300;
+            int bl = qlo[p][0], bh = qhi[p][0];
+            for (int a = 0; a < 3; ++a)
+                for (int c = 0; c < 3; ++c) {
+                    const int el = t.color_unq[crange][lo_c[a]], eh = t.color_unq[crange][hi_c[c]];
+                    double e = 0;
+                    for (int i : members[p]) {
+                        const float d = float(eh - el), x = in.x[i][0] * 255.0f - float(el);
+                        const float w = d != 0.0f ? std::clamp(x / d, 0.0f, 1.0f) * 64.0f : 0.0f;
+                        const int wq = t.weight_unq[gm.range][plan.nearest_weight[gm.range][std::clamp(int(std::lround(w)), 0, 64)]];
+                        const double v = (el * (64 - wq) + eh * wq) / 64.0 - in.x[i][0] * 255.0;
+                        e += v * v;
+                    }
+                    if (e < best_e) { best_e = e; bl = lo_c[a]; bh = hi_c[c]; }
+                }
+            qlo[p][0] = bl;
+            qhi[p][0] = bh;
+            elo[p][0] = t.color_unq[crange][bl];
+            ehi[p][0] = t.color_unq[crange][bh];
+            for (int i : members[p]) {
+                const float d = float(ehi[p][0] - elo[p][0]), x = in.x[i][0] * 255.0f - float(elo[p][0]);
+                const float w = d != 0.0f ? std::clamp(x / d, 0.0f, 1.0f) * 64.0f : 0.0f;
+                gridq[i] = plan.nearest_weight[gm.range][std::clamp(int(std::lround(w)), 0, 64)];
             }
         }
     }
@@ -524,16 +577,17 @@ void encode_block(const AkvTables& t, const float* texels, const EncoderOptions&
         for (int k = 0; k < in.nch; ++k) in.x[i][k] = in.full[i][in.ch[k]];
 
     const float q = opt.quality;
-    const int refine = q < 30 ? 0 : (q < 70 ? 1 : 2);
+    const int refine = q < 30 ? 0 : (q < 70 ? 1 : q < 90 ? 2 : 4);
     const int bx = int(t.block_x), by = int(t.block_y);
     Candidate best;
     // Identity grid, every weight range, for each partition layout tried.
     std::vector<PartitionLayout> layouts(1);
     if (q >= 30) {
-        const int max_parts = q >= 70 ? 3 : 2;
+        const int max_parts = q >= 90 ? 4 : q >= 70 ? 3 : 2;
         for (int k = 2; k <= max_parts; ++k) {
             if (k * 2 * ((in.cem >> 2) + 1) > 18) break;
-            for (int seed : best_seeds(plan, in, k, (q >= 70 && k == 2) ? 2 : 1)) {
+            const int keep = q >= 90 ? (k == 2 ? 4 : 2) : (q >= 70 && k == 2) ? 2 : 1;
+            for (int seed : best_seeds(plan, in, k, keep)) {
                 PartitionLayout pl;
                 pl.count = k;
                 pl.seed = seed;
@@ -547,7 +601,7 @@ void encode_block(const AkvTables& t, const float* texels, const EncoderOptions&
     for (size_t li = 0; li < layouts.size(); ++li) {
         double before = best.err;
         for (const GridMode& g : plan.modes)
-            if (g.identity) make_candidate(plan, in, layouts[li], g, refine, best);
+            if (g.identity) make_candidate(plan, in, layouts[li], g, refine, best, q >= 90);
         if (best.err < before) best_layout = int(li);
     }
     // Smaller weight grids for the winning layout at high effort.

@@ -322,7 +322,7 @@ def test_encoder_quality_against_astcenc_record(golden, pair):
     """Own encoder at quality 98 on the reference's captured, normalised V
     (fixed_input.npz of scripts/probe_block_geometry.py:142-155): the error
     tests/golden/encoder_quality.py recorded is reproduced, and stays within
-    1.35x of astcenc 5.7.0's recorded quality-98 error on the same image."""
+    1.15x of astcenc 5.7.0's recorded quality-98 error on the same image."""
     import json
     cap, layer = pair
     rec = next(r for r in json.loads((golden / "encoder_quality.json").read_text())["pairs"]
@@ -340,4 +340,4 @@ def test_encoder_quality_against_astcenc_record(golden, pair):
         enc.close()
     err = float(np.sum(np.square(np.stack(dec).astype(np.float64) - scalar)))
     assert err == pytest.approx(rec["this_q98"]["normalized_padded_error_sse"], rel=1e-9)
-    assert err <= 1.35 * rec["astcenc_q98"]["normalized_padded_error_sse"]
+    assert err <= 1.15 * rec["astcenc_q98"]["normalized_padded_error_sse"]
