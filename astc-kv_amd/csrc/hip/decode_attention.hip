@@ -50,6 +50,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
     // chunk's other loads, the rest just before the header stage (all arrive
     // during it; issued together they stall the chunk's first phase).
     constexpr int kKEarly = TPG < 2 ? TPG : 2;
+    constexpr bool kSpread = NCH == 1 || WIDE;
     __shared__ AstcShared<D, NCH, WIDE> sh;
     const AkvAttnParams& p = a.p;
     const Footprint f = a.fp;
@@ -110,6 +111,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
     for (int c0 = split_begin; c0 < split_end; c0 += CT) {
         const int ntok = min(CT, split_end - c0);
         const int ntiles = (ntok + 15) >> 4;
+        // Tiles per group: TPG, or, where chunks are mostly shorter than a
+        // round (TPG tiles for every wave: scalar layouts, the wide variant),
+        // as many as spread the chunk over all four waves.
+        const int gt = kSpread ? min(TPG, (ntiles + kWaves - 1) / kWaves) : TPG;
         const int nblk = chunk_blocks(c0);
         // 1. Loads. Only the blocks cross chunks (requested one chunk ahead:
         // the header stage needs them first). The rest is requested here and
@@ -135,7 +140,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
         const __amdgpu_buffer_rsrc_t krs = k_rsrc(c0);
         if constexpr (!DUMP) {
 #pragma unroll
-            for (int t = 0; t < kKEarly; ++t) load_k_tile<D>(kreg + t * C::kRowLoads, krs, 16 * (TPG * wave + t), lane);
+            for (int t = 0; t < kKEarly; ++t) load_k_tile<D>(kreg + t * C::kRowLoads, krs, 16 * (gt * wave + t), lane);
         }
         // 2. Block headers, with the chunk's blocks sorted by decode-path class
         // so that the lanes of a wave take the same branches. Each block's raw
@@ -166,7 +171,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
         if constexpr (!DUMP) {
 #pragma unroll
             for (int t = kKEarly; t < TPG; ++t)
-                load_k_tile<D>(kreg + t * C::kRowLoads, krs, 16 * (TPG * wave + t), lane);
+                load_k_tile<D>(kreg + t * C::kRowLoads, krs, 16 * (gt * wave + t), lane);
         }
         // What the texel stage needs besides the headers, written first so
         // that nothing of it stays in registers through the header stage:
@@ -209,7 +214,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
             __syncthreads();
             if (tid == 0) sh.nfill = 0;   // read by every thread before the barrier above
         }
-        // 3. This wave's groups of TPG consecutive tiles (every fourth group):
+        // 3. This wave's groups of gt consecutive tiles (every fourth group):
         // S for the whole group, then for each tile its texels straight into
         // MFMA operands and P.V. The next group's K rows are requested as soon
         // as S no longer needs the registers.
@@ -234,14 +239,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
             }
         } else {
 #pragma unroll 1
-            for (int tb0 = 16 * TPG * wave; tb0 < ntok; tb0 += 16 * TPG * kWaves) {
-                const int ng = min(TPG, (ntok - tb0 + 15) >> 4);
+            for (int tb0 = 16 * gt * wave; tb0 < ntok; tb0 += 16 * gt * kWaves) {
+                const int ng = min(gt, (ntok - tb0 + 15) >> 4);
                 uint32_t rows[4];   // token_row_entry of this lane's four tokens of the tile
                 attend_group<D, G, true, C::kRowBlocksPerGroup>(
                     Fp16KOperands<D>{kreg}, &sh.q[0][0], ng, tb0, ntok, sh.so, C::kMaxTok, st, [&](int t, int kc, half4* va) {
                         if (kc == 0) {
                             if (t == 0) {   // S is done with this group's K rows
-                                const int nb0 = tb0 + 16 * TPG * kWaves;
+                                const int nb0 = tb0 + 16 * gt * kWaves;
 #pragma unroll
                                 for (int tt = 0; tt < TPG; ++tt)
                                     load_k_tile<D>(kreg + tt * C::kRowLoads, krs, nb0 + 16 * tt, lane);

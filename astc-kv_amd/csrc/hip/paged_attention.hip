@@ -198,6 +198,9 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
     for (int c0 = split_begin; c0 < split_end; c0 += CT) {
         const int ntok = min(CT, split_end - c0);
         const int ntiles = (ntok + 15) >> 4;
+        // Tiles per group: TPG, or as many as spread a chunk of less than a
+        // round (TPG tiles for every wave) over all four waves.
+        const int gt = min(TPG, (ntiles + kWaves - 1) / kWaves);
         const int nastc = chunk_astc(c0);
         const int nblk = chunk_blocks(c0);
         // 1. Loads. Only the blocks cross chunks (requested one chunk ahead:
@@ -222,7 +225,8 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
         }
         if (c0 + CT < split_end) raw = load_blk(c0 + CT, chunk_blocks(c0 + CT), false);
 #pragma unroll
-        for (int t = 0; t < kKEarly; ++t) load_k(kw + t * kKWords, c0, 16 * (TPG * wave + t));
+        for (int t = 0; t < kKEarly; ++t)
+            if (t < gt) load_k(kw + t * kKWords, c0, 16 * (gt * wave + t));
         // 2. Block headers (the blocks of the chunk's ASTC tokens), sorted by
         // decode-path class.
         int key = 0, rank = 0;
@@ -266,19 +270,21 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
         __syncthreads();
         // 3. Tile groups; tiles at or past `full` read V from the FP16 tail.
 #pragma unroll
-        for (int t = kKEarly; t < TPG; ++t) load_k(kw + t * kKWords, c0, 16 * (TPG * wave + t));
+        for (int t = kKEarly; t < TPG; ++t)
+            if (t < gt) load_k(kw + t * kKWords, c0, 16 * (gt * wave + t));
 #pragma unroll 1
-        for (int tb0 = 16 * TPG * wave; tb0 < ntok; tb0 += 16 * TPG * kWaves) {
-            const int ng = min(TPG, (ntok - tb0 + 15) >> 4);
+        for (int tb0 = 16 * gt * wave; tb0 < ntok; tb0 += 16 * gt * kWaves) {
+            const int ng = min(gt, (ntok - tb0 + 15) >> 4);
             uint32_t rows[4];
             int trow[4];
             bool in_tail = false;
             auto vtile = [&](int t, int kc, half4* va) {
                 if (kc == 0) {
                     if (t == 0) {   // S is done with this group's K rows
-                        const int nb0 = tb0 + 16 * TPG * kWaves;
+                        const int nb0 = tb0 + 16 * gt * kWaves;
 #pragma unroll
-                        for (int tt = 0; tt < TPG; ++tt) load_k(kw + tt * kKWords, c0, nb0 + 16 * tt);
+                        for (int tt = 0; tt < TPG; ++tt)
+                            if (tt < gt) load_k(kw + tt * kKWords, c0, nb0 + 16 * tt);
                     }
                     in_tail = c0 + tb0 + 16 * t >= full;
                     if (in_tail) {
