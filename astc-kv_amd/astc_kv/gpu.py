@@ -114,10 +114,11 @@ def default_tile(batch: int, kv_heads: int, tokens: int, chunk: int, block: int 
     """Tokens per split (a multiple of `block`: 16 for the kernels here).
 
     * Fewer chunks than CUs: splits of about tokens * batch * kv_heads / CUs
-      tokens (at least 16) for parallelism, but at most 24 splits per
-      sequence (the merge reads every split's state: T2048 batch 1 runs in
-      19 us with 64 splits, 16.6 us with 16, 13.3 us for T384 with 24);
-      above 64 tokens, whole groups of four tiles (multiples of 64).
+      tokens (at least 16) for parallelism, but at most 32 splits per
+      sequence (the merge reads every split's state; the reference's scalar
+      6x6 payload at batch 1: T2048 19.2 us with 32 splits, 20.8 us with 16;
+      T384 17.9 us with 24); above 64 tokens, whole groups of four tiles
+      (multiples of 64).
     * Up to 32 rounds of one-chunk workgroups (groups_per_cu per CU): the
       tile (at most 16 chunks) minimising rounds x (tile + overhead_tokens),
       i.e. the time of the last workgroup to finish when each costs its tokens
@@ -131,7 +132,7 @@ def default_tile(batch: int, kv_heads: int, tokens: int, chunk: int, block: int 
     slots = groups_per_cu * cu_count
     total = seqs * -(-tokens // chunk)
     if total < cu_count:
-        want = max(16, -(-tokens * seqs // cu_count), -(-tokens // 24))
+        want = max(16, -(-tokens * seqs // cu_count), -(-tokens // 32))
         step = 64 if want > 64 else block
         return min(chunk, -(-want // step) * step)
     if total <= 32 * slots:

@@ -275,11 +275,11 @@ def test_default_tiles():
     t = default_tile(8, 8, 32768, 128, 16, groups_per_cu=2)
     assert t == 2048 and 64 * -(-32768 // t) == 2 * 512
     # Tiny workloads: split for parallelism, in whole tiles, never above a
-    # chunk, at most 24 splits per sequence.
+    # chunk, at most 32 splits per sequence.
     t = default_tile(1, 3, 384, 256, 16)
     assert t == 16 and -(-384 // t) == 24
     t = default_tile(1, 3, 2048, 128, 16)
-    assert t % 16 == 0 and t <= 128 and -(-2048 // t) <= 24
+    assert t == 64 and -(-2048 // t) == 32
     assert tile_for_splits(2048, 8, 6, 64) == 256 and -(-2048 // 256) == 8
     p = fp16_params(16, 3, 9, 8192, 64)
     assert p.tile_tokens == 512 and p.splits == 16
