@@ -39,7 +39,7 @@
 
 namespace akv_hip {
 
-template <int D, int NCH, int G, bool DUMP, bool WIDE>
+template <int D, int NCH, int G, bool DUMP, bool WIDE, bool SPREAD>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 64 ? AKV_ASTC_WAVES : 2))) void astc_attn_kernel(
     KernelArgs a, const float* __restrict__ q, const uint16_t* __restrict__ k, const uint4* __restrict__ vblk,
     const uint16_t* __restrict__ vscale, const uint16_t* __restrict__ voffset, const AkvTables* __restrict__ tab,
@@ -50,7 +50,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
     // chunk's other loads, the rest just before the header stage (all arrive
     // during it; issued together they stall the chunk's first phase).
     constexpr int kKEarly = TPG < 2 ? TPG : 2;
-    constexpr bool kSpread = NCH == 1 || WIDE;
     __shared__ AstcShared<D, NCH, WIDE> sh;
     const AkvAttnParams& p = a.p;
     const Footprint f = a.fp;
@@ -111,10 +110,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
     for (int c0 = split_begin; c0 < split_end; c0 += CT) {
         const int ntok = min(CT, split_end - c0);
         const int ntiles = (ntok + 15) >> 4;
-        // Tiles per group: TPG, or, where chunks are mostly shorter than a
-        // round (TPG tiles for every wave: scalar layouts, the wide variant),
-        // as many as spread the chunk over all four waves.
-        const int gt = kSpread ? min(TPG, (ntiles + kWaves - 1) / kWaves) : TPG;
+        // Tiles per group: TPG, or, in the variant for chunks shorter than a
+        // round (TPG tiles for every wave), as many as spread the chunk over
+        // all four waves.
+        const int gt = SPREAD ? min(TPG, (ntiles + kWaves - 1) / kWaves) : TPG;
         const int nblk = chunk_blocks(c0);
         // 1. Loads. Only the blocks cross chunks (requested one chunk ahead:
         // the header stage needs them first). The rest is requested here and
@@ -585,20 +584,20 @@ struct Ptrs {
     uint32_t* arrivals = nullptr;     // non-null: merge in the split kernel
 };
 
-template <int D, int NCH, bool DUMP, bool WIDE>
+template <int D, int NCH, bool DUMP, bool WIDE, bool SPREAD>
 hipError_t launch_astc_g(const KernelArgs& a, uint32_t G, const Ptrs& x, hipStream_t st) {
     dim3 grid(a.p.splits, a.p.kv_heads, a.p.batch);
     auto* s2 = reinterpret_cast<float2*>(x.stats);
     if constexpr (DUMP) {
-        astc_attn_kernel<D, NCH, 1, true, WIDE><<<grid, kThreads, 0, st>>>(a, x.q, x.k, x.vblk, x.vs, x.vo, x.tab, x.partial,
+        astc_attn_kernel<D, NCH, 1, true, WIDE, SPREAD><<<grid, kThreads, 0, st>>>(a, x.q, x.k, x.vblk, x.vs, x.vo, x.tab, x.partial,
                                                                       s2, x.dump, nullptr, nullptr);
         return hipGetLastError();
     }
     switch (G) {
 #define AKV_CASE(GG)                                                                                       \
     case GG:                                                                                               \
-        astc_attn_kernel<D, NCH, GG, DUMP, WIDE><<<grid, kThreads, 0, st>>>(a, x.q, x.k, x.vblk, x.vs, x.vo, x.tab, \
-                                                                       x.partial, s2, x.dump, x.out,      \
+        astc_attn_kernel<D, NCH, GG, DUMP, WIDE, SPREAD><<<grid, kThreads, 0, st>>>(a, x.q, x.k, x.vblk, x.vs, x.vo, \
+                                                                               x.tab, x.partial, s2, x.dump, x.out, \
                                                                        x.arrivals);                       \
         break;
         AKV_CASE(1)
@@ -616,12 +615,24 @@ hipError_t launch_astc_g(const KernelArgs& a, uint32_t G, const Ptrs& x, hipStre
 template <bool DUMP>
 hipError_t launch_astc(const KernelArgs& a, uint32_t G, const Ptrs& x, hipStream_t st) {
     const bool scalar = a.p.layout == AKV_LAYOUT_SCALAR;
+    // SPREAD: the variant whose tile groups shrink for chunks shorter than a
+    // round (TPG tiles for every wave). Scalar layouts (11 or 22 block
+    // columns) and the wide variant have such chunks; RGBA ones mostly do not
+    // (6x5 at head dim 64 and every footprint at 128 fill whole rounds), and
+    // there the fixed group is kept, which the compiler schedules better.
     if (a.p.dim == 64) {
         if (a.wide)
-            return scalar ? launch_astc_g<64, 1, DUMP, true>(a, G, x, st) : launch_astc_g<64, 4, DUMP, true>(a, G, x, st);
-        return scalar ? launch_astc_g<64, 1, DUMP, false>(a, G, x, st) : launch_astc_g<64, 4, DUMP, false>(a, G, x, st);
+            return scalar ? launch_astc_g<64, 1, DUMP, true, true>(a, G, x, st)
+                          : launch_astc_g<64, 4, DUMP, true, true>(a, G, x, st);
+        if (scalar) return launch_astc_g<64, 1, DUMP, false, true>(a, G, x, st);
+        if constexpr (!DUMP) {
+            const uint32_t round = 16u * (G <= 4 ? 4u : 2u) * kWaves;   // tokens
+            if (a.chunk_tokens % round) return launch_astc_g<64, 4, false, false, true>(a, G, x, st);
+        }
+        return launch_astc_g<64, 4, DUMP, false, false>(a, G, x, st);
     }
-    return scalar ? launch_astc_g<128, 1, DUMP, false>(a, G, x, st) : launch_astc_g<128, 4, DUMP, false>(a, G, x, st);
+    return scalar ? launch_astc_g<128, 1, DUMP, false, true>(a, G, x, st)
+                  : launch_astc_g<128, 4, DUMP, false, false>(a, G, x, st);
 }
 
 template <int D>
