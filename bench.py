@@ -335,7 +335,7 @@ def _counter_means(directory: str, counter: str):
 
 
 def _is_split_kernel(name: str) -> bool:
-    """astc_attn_kernel<D, NCH, G, DUMP, WIDE> with DUMP false (not the decode
+    """astc_attn_kernel<D, NCH, G, DUMP, WIDE, SPREAD> with DUMP false (not the decode
     readback), or the paged kernel paged_attn_kernel<D, NCH, G, KU4>."""
     if name.startswith("paged_attn_kernel<"):
         return True
