@@ -318,11 +318,24 @@ __device__ __attribute__((always_inline)) inline void weight_fields(const uint32
     static_assert(V * nb <= 160, "weight fields fit five words");
 #pragma unroll
     for (int i = 0; i < 5; ++i) q[i] = 0;
-    ise_unpack<R, V>(s, L, vlim, [&](auto ji, uint32_t v) {
-        constexpr int P = decltype(ji)::value * nb, w = P >> 5, o = P & 31;
-        q[w] |= v << o;
-        if constexpr (o + nb > 32) q[w + 1] |= v >> (32 - o);
-    });
+    if constexpr ((e.trit || e.quint) && e.bits == 0) {
+        // No plain bits: a group's table entry (digit j at bit nb * j) is
+        // already its fields, so each group is one lookup and one insert.
+        constexpr int gs = e.trit ? 5 : 3, gb = e.trit ? 8 : 7;
+        static_assert(((V + gs - 1) / gs) * gs * nb <= 160, "whole groups fit five words");
+        ise_groups<gs, (V + gs - 1) / gs>(vlim, [&](auto gi) {
+            constexpr int g = decltype(gi)::value, P = g * gs * nb, w = P >> 5, o = P & 31;
+            const uint32_t dig = e.trit ? L.trit[bits_at<g * gb, gb>(s)] : L.quint[bits_at<g * gb, gb>(s)];
+            q[w] |= dig << o;
+            if constexpr (o + gs * nb > 32) q[w + 1] |= dig >> (32 - o);
+        });
+    } else {
+        ise_unpack<R, V>(s, L, vlim, [&](auto ji, uint32_t v) {
+            constexpr int P = decltype(ji)::value * nb, w = P >> 5, o = P & 31;
+            q[w] |= v << o;
+            if constexpr (o + nb > 32) q[w + 1] |= v >> (32 - o);
+        });
+    }
 }
 
 // Colour integer sequence of this lane's block: range `crange`, `nv` values
