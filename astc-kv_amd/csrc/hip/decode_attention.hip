@@ -39,8 +39,11 @@
 
 namespace akv_hip {
 
+// Occupancy: three workgroups per CU at head dim 64, two at 128; the wide
+// variant runs at most one per CU.
 template <int D, int NCH, int G, bool DUMP, bool WIDE, bool SPREAD>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 64 ? AKV_ASTC_WAVES : 2))) void astc_attn_kernel(
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(D == 64 && !WIDE ? AKV_ASTC_WAVES : WIDE ? 1 : 2))) void astc_attn_kernel(
     KernelArgs a, const float* __restrict__ q, const uint16_t* __restrict__ k, const uint4* __restrict__ vblk,
     const uint16_t* __restrict__ vscale, const uint16_t* __restrict__ voffset, const AkvTables* __restrict__ tab,
     float* partial, float2* stats, uint16_t* __restrict__ dump, float* __restrict__ out, uint32_t* arrivals) {
