@@ -32,11 +32,12 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // WIDE: the launch has at most one workgroup per CU (small batches, few
 // splits), so LDS has room for a full 256-block chunk at head dim 64 too:
 // fewer chunks, hence a shorter critical path, per split.
-template <int D, int NCH, bool WIDE = false>
+// MAXB: blocks per chunk when not 0 (a kernel that needs less LDS).
+template <int D, int NCH, bool WIDE = false, int MAXB = 0>
 struct Cfg {
     // Blocks per chunk (header stage, one per lane): at head dim 128 the
     // kernel runs two workgroups per CU, which leaves room for a full 256.
-    static constexpr int kMaxBlocks = (D == 64 && !WIDE) ? 160 : 256;
+    static constexpr int kMaxBlocks = MAXB ? MAXB : (D == 64 && !WIDE) ? 160 : 256;
     static constexpr int kMaxTok = D == 64 ? 320 : 128;          // tokens per chunk
     static constexpr int kMaxTiles = kMaxTok / 16;
     static constexpr int kWaveTiles = kMaxTiles / kWaves;        // tiles per wave per chunk
@@ -270,11 +271,12 @@ struct U4KOperands {
     }
 };
 
-template <int D, int G, bool AFFINE, int MPB, typename KOp, typename VTile>
+template <int D, int G, bool AFFINE, int MPB, int TPGMAX = Grp<G, D>::TPG, typename KOp, typename VTile>
 __device__ __attribute__((always_inline)) inline void attend_group(const KOp& kop, const uint2* qs, int ng, int tb0,
                                                                    int ntok, const uint32_t* so, int so_cap,
                                                                    AttnState<D>& st, VTile&& vtile) {
-    constexpr int Gs = Grp<G, D>::Gs, TPG = Grp<G, D>::TPG;
+    constexpr int Gs = Grp<G, D>::Gs, TPG = TPGMAX;   // TPGMAX <= Grp's TPG: fewer tiles per group
+    static_assert(TPGMAX >= 1 && TPGMAX <= Grp<G, D>::TPG, "tiles per group");
     const int lane = threadIdx.x & 63, n16 = lane & 15, g = lane >> 4;
     const int rt = n16 / Gs, h = n16 % Gs;   // this lane's row of S and P: tile, head
     // S^T = K . Q^T per tile, K rows as the A operand and Q as the B operand:
@@ -545,9 +547,9 @@ __device__ inline void combine_waves(float* comb, WaveStats& ws, AttnState<D>& s
 
 // FILLS: room for the fill stage's texels (the split kernel's; the paged
 // kernel has no fill stage).
-template <int D, int NCH, bool WIDE = false, bool FILLS = true>
+template <int D, int NCH, bool WIDE = false, bool FILLS = true, int MAXB = 0>
 struct AstcShared {
-    using C = Cfg<D, NCH, WIDE>;
+    using C = Cfg<D, NCH, WIDE, MAXB>;
     LdsTables tabs;
     union {
         struct {

@@ -41,9 +41,21 @@ struct PagedArgs {
     float qscale;
 };
 
+// Head dim 128, scalar layout: three workgroups per CU rather than two, for
+// a kernel that waits on header-stage latency most of its cycles. That fits
+// with one tile per group (168 VGPRs) and chunks of at most 192 blocks (52 KB
+// of LDS; scalar 6x6 chunks are 176 blocks either way). Ragged 64-sequence
+// batch, D128, 4-bit K + scalar 6x6 V at quality 50: 2.02 -> 1.53 ms.
+template <int D, int NCH>
+struct PagedCfg {
+    static constexpr bool kThree = D == 128 && NCH == 1;
+    static constexpr int kMaxBlocks = kThree ? 192 : 0;   // 0: Cfg's own
+    static constexpr int kWavesPerSimd = D == 64 ? AKV_ASTC_WAVES : kThree ? 3 : 2;
+};
+
 template <int D, int NCH>
 struct PagedShared {
-    AstcShared<D, NCH, false, false> a;
+    AstcShared<D, NCH, false, false, PagedCfg<D, NCH>::kMaxBlocks> a;
     int32_t pages[kMaxSplitPages];     // the split's pages, from its first
 };
 
@@ -60,21 +72,21 @@ __device__ inline void tail_texels(const uint16_t* __restrict__ tail, const int 
 }
 
 template <int D, int NCH, int G, bool KU4>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 64 ? AKV_ASTC_WAVES : 2))) void
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PagedCfg<D, NCH>::kWavesPerSimd))) void
 paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restrict__ kpool,
                   const uint16_t* __restrict__ kmeta, const uint4* __restrict__ vpool,
                   const uint16_t* __restrict__ vscale, const uint16_t* __restrict__ voffset,
                   const int32_t* __restrict__ table, const int32_t* __restrict__ lens,
                   const uint16_t* __restrict__ vtail, const AkvTables* __restrict__ tab, float* partial,
                   float2* stats, float* __restrict__ out, uint32_t* arrivals) {
-    using C = Cfg<D, NCH>;
-    constexpr int TPG = Grp<G, D>::TPG;
+    using C = Cfg<D, NCH, false, PagedCfg<D, NCH>::kMaxBlocks>;
+    constexpr int TPG = PagedCfg<D, NCH>::kThree ? 1 : Grp<G, D>::TPG;   // tiles per group
     constexpr int kKEarly = TPG < 2 ? TPG : 2;
     // Per tile and lane: FP16 K, D/32 16-byte row pieces; 4-bit K, D/32 code
     // dwords and D/32 (offset, scale) dwords.
     constexpr int kKWords = KU4 ? D / 16 : 4 * (D / 32);
     __shared__ PagedShared<D, NCH> shp;
-    AstcShared<D, NCH, false, false>& sh = shp.a;
+    AstcShared<D, NCH, false, false, PagedCfg<D, NCH>::kMaxBlocks>& sh = shp.a;
     const AkvPagedParams& p = a.p;
     const Footprint f = a.fp;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -300,10 +312,10 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
                 texel_operands<NCH>(tv, va);
             };
             if constexpr (KU4)
-                attend_group<D, G, true, C::kRowBlocksPerGroup>(U4KOperands<D>{kw}, &sh.q[0][0], ng, tb0, ntok,
+                attend_group<D, G, true, C::kRowBlocksPerGroup, TPG>(U4KOperands<D>{kw}, &sh.q[0][0], ng, tb0, ntok,
                                                                  sh.so, C::kMaxTok, st, vtile);
             else
-                attend_group<D, G, true, C::kRowBlocksPerGroup>(
+                attend_group<D, G, true, C::kRowBlocksPerGroup, TPG>(
                     Fp16KOperands<D>{reinterpret_cast<const uint4*>(kw)}, &sh.q[0][0], ng, tb0, ntok, sh.so,
                     C::kMaxTok, st, vtile);
         }
@@ -459,7 +471,7 @@ int check_paged(const AkvPagedParams* p, uint32_t* G) {
 // lcm(16, block_y) tokens) whose blocks fit the header stage.
 template <int D, int NCH>
 int plan_paged(const AkvPagedParams* p, PagedArgs* a) {
-    using C = Cfg<D, NCH>;
+    using C = Cfg<D, NCH, false, PagedCfg<D, NCH>::kMaxBlocks>;
     const uint32_t by = p->block_y;
     uint32_t step = 16;
     while (step % by) step += 16;
