@@ -17,8 +17,10 @@
 //   2. header stage, one lane per block, blocks sorted by decode-path class:
 //      BlockDesc records in LDS;
 //   3. each wave takes every fourth group of consecutive 16-token tiles
-//      (attend_group): S for the group on the matrix cores, the online
-//      softmax, then per tile its texels decoded straight into P.V operands.
+//      (attend_group; in the SPREAD variant a chunk shorter than four whole
+//      groups is cut into smaller ones, so that every wave gets tiles): S for
+//      the group on the matrix cores, the online softmax, then per tile its
+//      texels decoded straight into P.V operands.
 // At the end the four wave states are combined into the split's state; the
 // last split workgroup of each (sequence, kv head) merges when the caller
 // passes arrival counters, otherwise merge_kernel does.

@@ -10,7 +10,8 @@
 // changes is addressing: every block row, K row and scale/offset is found
 // through the split's pages (cached in LDS), chunks and tiles are aligned to
 // 16 tokens so that a tile never straddles a page, and tiles past the last
-// full page read V from the FP16 tail with scale 1 and offset 0.
+// full page read V from the FP16 tail with scale 1 and offset 0. At head dim
+// 128 with a scalar layout the kernel runs three workgroups per CU (PagedCfg).
 //
 // Reference semantics: metal/attention_gqa_v10.metal:568-674 and :229-253 (as
 // the contiguous kernel); 4-bit K as affine_quantize(axis="token", group=32),
