@@ -280,6 +280,11 @@ def test_default_tiles():
     assert t == 16 and -(-384 // t) == 24
     t = default_tile(1, 3, 2048, 128, 16)
     assert t == 64 and -(-2048 // t) == 32
+    # T8192 at batch 1 (192 one-chunk workgroups of 128 tokens): the chunk
+    # caps the split; more splits (tile 64: 29.7 us) or fewer (tile 256:
+    # 35.0 us) measured slower on the reference's payload than 128 (24.4 us).
+    t = default_tile(1, 3, 8192, 128, 16)
+    assert t == 128 and -(-8192 // t) == 64
     assert tile_for_splits(2048, 8, 6, 64) == 256 and -(-2048 // 256) == 8
     p = fp16_params(16, 3, 9, 8192, 64)
     assert p.tile_tokens == 512 and p.splits == 16
