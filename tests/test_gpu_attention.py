@@ -111,6 +111,27 @@ def test_synthetic_attention(gpu, layout, block, b, hq, hkv, t, d, heavy):
         check(run(gpu, q, k, atlas, tile), q, k, vr)
 
 
+@pytest.mark.parametrize("layout,block,hq,hkv,t,d,tiles", [
+    # chunks that are not whole rounds of tile groups: 160-token (4x4) and
+    # 192-token (5x5) chunks at head dim 64, 64-token scalar chunks at 128,
+    # and splits that end inside a chunk or a tile
+    ("rgba", (4, 4), 9, 3, 700, 64, (7, 40, 160, 333)),
+    ("rgba", (5, 5), 12, 3, 650, 64, (None, 96, 250)),
+    ("scalar", (6, 6), 32, 8, 400, 128, (None, 13, 80)),
+])
+def test_tile_groups_of_short_chunks(gpu, layout, block, hq, hkv, t, d, tiles):
+    """The split kernel's tile groups shrink for chunks shorter than four
+    whole groups (every wave gets tiles); results as the oracle's at any tile."""
+    from astc_kv.atlas import build_atlas
+    rng = np.random.default_rng(t + d + hq)
+    q, k, v = synthetic(rng, 1, hq, hkv, t, d)
+    atlas = build_atlas(v, layout, block, page_tokens=120 if block[1] in (5, 6) else 128, quality=60)
+    vr = oracle_v(atlas)
+    for tile in tiles:
+        print(f"{layout} {block} T{t} D{d} tile {tile}", flush=True)
+        check(run(gpu, q, k, atlas, tile), q, k, vr)
+
+
 def test_split_states_match_oracle(gpu, golden):
     """partial/stats of every split against the FP64 split-state oracle."""
     from astc_kv.atlas import atlas_from_manifest
