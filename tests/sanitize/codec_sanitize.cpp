@@ -69,6 +69,16 @@ int main(int argc, char** argv) {
                 std::fprintf(stderr, "%dx%d q%g image decode differs\n", bx, by, quality);
                 ++bad;
             }
+            // The scalar layout's images (grey RGB, alpha 1: luminance
+            // endpoint modes, and at quality 90+ the endpoint polish).
+            for (size_t i = 0; i < img.size(); i += 4) img[i + 1] = img[i + 2] = img[i], img[i + 3] = 1.0f;
+            bad += check(akv_encode(ctx, img.data(), w, h, payload.data(), payload.size()), "encode grey");
+            bad += check(akv_decode(ctx, payload.data(), payload.size(), dec.data(), w, h), "decode grey");
+            oracle_decode_image(payload.data(), long(payload.size()), bx, by, int(w), int(h), ref.data());
+            if (std::memcmp(dec.data(), ref.data(), dec.size() * sizeof(float))) {
+                std::fprintf(stderr, "%dx%d q%g grey image decode differs\n", bx, by, quality);
+                ++bad;
+            }
             // Texel blocks straight through akv_encode_blocks.
             std::vector<float> tex(size_t(8) * nt * 4);
             for (auto& v : tex) v = u(rng);
