@@ -685,7 +685,20 @@ __device__ inline uint4 block_part_words(uint4 raw, uint4 words) {
 // texels is marked kInfoFilled: the caller gives it a slot of its fill area
 // (or clears the mark) and runs fill_values before the texel stage.
 // CCAP: decode_colour_values<true> (colour values up to the pass's largest count).
-template <int NCH, bool CAP = false, bool FILL = false, bool CCAP = false>
+// Bits of a weight field as the header stores it (a value of weight range
+// r: its plain bits, plus 2 for a trit, 3 for a quint), four bits per range:
+// decode_header's NBC variant uses it instead of the table read, whose value
+// the register-tight paged kernel spilled across the colour decode.
+constexpr uint64_t weight_field_bits() {
+    uint64_t t = 0;
+    for (int r = 0; r < 12; ++r)
+        t |= uint64_t(akv::kIse[r].bits + (akv::kIse[r].trit ? 2 : akv::kIse[r].quint ? 3 : 0)) << (4 * r);
+    return t;
+}
+inline constexpr uint64_t kWeightFieldBits = weight_field_bits();
+static_assert(kWeightFieldBits == 0x555444333221ull, "field bits of weight ranges 0-11");
+
+template <int NCH, bool CAP = false, bool FILL = false, bool CCAP = false, bool NBC = false>
 __device__ __attribute__((always_inline)) inline void decode_header(const LdsTables& L, BlockDesc<NCH>& d,
                                                                    uint32_t* cv, int ntex = 0) {
     const uint32_t* blk = d.tab;        // block bits
@@ -753,8 +766,13 @@ __device__ __attribute__((always_inline)) inline void decode_header(const LdsTab
     // Weights: the integer sequence runs from bit 127 downwards, so in the
     // bit-reversed block it starts at bit 0; unpacked to nb-bit fields.
     const int wrange = int(akv::mode_range(md));
-    const uint32_t wi = L.ise[wrange];
-    const int nb = int(wi & 0xFF) + ((wi & 0x100) ? 2 : (wi & 0x200) ? 3 : 0);
+    int nb;
+    if constexpr (NBC) {
+        nb = int((kWeightFieldBits >> (4 * wrange)) & 15u);
+    } else {
+        const uint32_t wi = L.ise[wrange];
+        nb = int(wi & 0xFF) + ((wi & 0x100) ? 2 : (wi & 0x200) ? 3 : 0);
+    }
     {
         uint32_t q[5];
         const int count = int(akv::mode_gw(md) * akv::mode_gh(md)) << (dual ? 1 : 0);

@@ -139,7 +139,12 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
     // its page ids from the block table, later ones from LDS.
     auto load_blk = [&](int c0, int nblk, bool from_table) -> uint4 {
         if (tid >= nblk) return uint4{0, 0, 0, 0};
-        const int r = int(fdiv(uint32_t(tid), a.mag_cols)), col = tid - r * cols;
+        // Recomputed per call: hoisted out of the chunk loop, the lane's
+        // 64-bit column address stayed live through the header stage and was
+        // spilled there.
+        int lt = tid;
+        asm volatile("" : "+v"(lt));
+        const int r = int(fdiv(uint32_t(lt), a.mag_cols)), col = lt - r * cols;
         // (c0 - base_tok) / by can exceed the 8-bit quotients fdiv is exact
         // for; c0 and base_tok are uniform, so this is one scalar division.
         const int grow = (c0 - base_tok) / by + r;
@@ -278,7 +283,7 @@ paged_attn_kernel(PagedArgs a, const float* __restrict__ q, const void* __restri
         }
         if (tid < nblk) {
             const int bi = sh.order[tid];
-            decode_header<NCH, false, false, D == 128 && NCH == 1>(sh.tabs, sh.u.h.desc[bi], sh.u.h.cv[tid]);
+            decode_header<NCH, false, false, D == 128 && NCH == 1, true>(sh.tabs, sh.u.h.desc[bi], sh.u.h.cv[tid]);
         }
         __syncthreads();
         // 3. Tile groups; tiles at or past `full` read V from the FP16 tail.
