@@ -31,6 +31,12 @@ CASES = [
     ("rgba", (6, 5), 80, 64, 9, 3, "fp16", True),
     ("scalar", (6, 6), 96, 64, 9, 3, "u4g32", True),
     ("rgba", (8, 8), 64, 64, 8, 1, "u4g32", False),
+    # scalar at head dim 128 (three workgroups per CU, one tile per group)
+    # with the other GQA group sizes and FP16 K
+    ("scalar", (6, 6), 96, 128, 3, 3, "fp16", True),     # G = 1
+    ("scalar", (6, 6), 96, 128, 6, 3, "u4g32", False),   # G = 2
+    ("scalar", (6, 6), 48, 128, 9, 3, "u4g32", True),    # G = 3
+    ("scalar", (6, 6), 96, 128, 16, 2, "fp16", False),   # G = 8
 ]
 
 
